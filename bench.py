@@ -1,0 +1,314 @@
+"""Benchmark of the KV-cache migration hot path on one MI355X.
+
+Default workload (N=1): config 2 - 16 requests with lognormal(median 1024,
+sigma 1.0) token counts clipped to [128, 8192], Llama-3-8B KV shape (32
+layers, 8 KV heads, head_dim 128, page 16), bf16, 16384-page source and
+destination pools, fragmented source free list.  One step = pack every
+request's pages from all layers into the contiguous transfer buffer, then
+unpack the buffer into the destination pages (the reference's
+get_kv_cache + insert_kv_cache, moved on-device).
+
+value = 4 * payload / elapsed, in GB/s (1e9 B/s): pack reads and writes the
+payload, unpack reads and writes it; elapsed is measured with HIP events on
+the stream the kernels run on, over the K timed steps.  Inputs are resident in
+HBM before timing starts.  Also reported: the roofline of the copy kernel
+(algorithmic bytes per launch / mean launch time vs 8 TB/s), p50/p90 promote
+latency of one 4096-token request (dst allocation + remap + block-table H2D +
+pack + unpack, to completion) and the reference's CPU path (torch
+index_select / index_copy_ on host tensors) timed on a bounded sample on this
+host's cores.
+
+Usage: python bench.py [--steps K] [--warmup W] [--workload 1..5]
+       [--no-cpu] [--no-promote] [--verify]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "KV pack+unpack GB/s (% of HBM peak); p50 promote latency, 4k-token request"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--mode", default="buffer", choices=["buffer", "fused"],
+                    help="buffer: pack + unpack (the metric); fused: pool-to-pool move")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-promote", action="store_true")
+    ap.add_argument("--verify", action="store_true", help="check the result against torch's gather/scatter")
+    ap.add_argument("--cpu-layers", type=int, default=0, help="layers in the CPU sample (0 = auto)")
+    return ap.parse_args()
+
+
+def device_setup(w, dev):
+    import torch
+
+    from paceserve_amd import workloads
+    from paceserve_amd.core.block_manager import BlockAllocator
+    from paceserve_amd.kv_transfer import migrate, ops
+
+    src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev)
+    dst = workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev)
+    alloc = BlockAllocator(w.shape.page_size, w.dst_pool_pages, w.dst_free)
+    plan = migrate.plan_batch(w.src_tables, w.src_pool_pages, alloc)
+    s_ids = torch.tensor(plan.src_ids, dtype=torch.int32, device=dev)
+    d_ids = torch.tensor(plan.dst_ids, dtype=torch.int32, device=dev)
+    return ops.PagedPool(src), ops.PagedPool(dst), plan, s_ids, d_ids
+
+
+def run_device(args, w, dev, src, dst, plan, s_ids, d_ids):
+    """Times K steps of pack + unpack (or fused move) with HIP events."""
+    import torch
+
+    from paceserve_amd.kv_transfer import ops
+
+    L = w.shape.num_layers
+    n = plan.n_pages
+    k = w.layers_per_chunk or L
+    buf = torch.empty((min(k, L), n) + w.shape.page_shape, dtype=w.shape.dtype, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step(evs):
+        for lb in range(0, L, k):
+            le = min(L, lb + k)
+            if args.mode == "fused":
+                evs.append(("move", le - lb, torch.cuda.Event(enable_timing=True)))
+                evs[-1][2].record(stream)
+                ops.move(src, s_ids, dst, d_ids, layer_begin=lb, layer_end=le)
+            else:
+                b = buf[: le - lb]
+                evs.append(("pack", le - lb, torch.cuda.Event(enable_timing=True)))
+                evs[-1][2].record(stream)
+                ops.pack(src, s_ids, b, layer_begin=lb, layer_end=le)
+                evs.append(("unpack", le - lb, torch.cuda.Event(enable_timing=True)))
+                evs[-1][2].record(stream)
+                ops.unpack(b, dst, d_ids, layer_begin=lb, layer_end=le)
+        end = torch.cuda.Event(enable_timing=True)
+        end.record(stream)
+        evs.append(("end", 0, end))
+
+    for _ in range(args.warmup):
+        step([])
+    torch.cuda.synchronize()
+    log(f"{w.name}: {n} pages x {L} layers, payload {w.payload_bytes / 2**30:.3f} GiB; warmup done")
+
+    evs = []
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        step(evs)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    elapsed_ms = start.elapsed_time(evs[-1][2])
+
+    # Per-launch durations: each recorded event opens one launch; the next
+    # event closes it.
+    launch_ms = {"pack": [], "unpack": [], "move": []}
+    launch_layers = {"pack": [], "unpack": [], "move": []}
+    for (kind, layers, ev), (_, _, nxt) in zip(evs[:-1], evs[1:]):
+        if kind in launch_ms:
+            launch_ms[kind].append(ev.elapsed_time(nxt))
+            launch_layers[kind].append(layers)
+
+    traffic_factor = 2 if args.mode == "fused" else 4
+    value = traffic_factor * w.payload_bytes * args.steps / (elapsed_ms / 1e3) / 1e9
+    kinds = ["move"] if args.mode == "fused" else ["pack", "unpack"]
+    durs = [d for kd in kinds for d in launch_ms[kd]]
+    lays = [x for kd in kinds for x in launch_layers[kd]]
+    # algorithmic bytes per launch: read + write of its layers' pages
+    bytes_per_launch = [2 * x * n * w.shape.page_bytes for x in lays]
+    achieved = (sum(bytes_per_launch) / len(bytes_per_launch)) / (statistics.mean(durs) / 1e3) / 1e9
+    res = {
+        "value": value,
+        "elapsed_ms": elapsed_ms,
+        "ms_per_step": wall * 1e3 / args.steps,
+        "event_ms_per_step": elapsed_ms / args.steps,
+        "pack_ms_mean": statistics.mean(launch_ms["pack"]) if launch_ms["pack"] else None,
+        "unpack_ms_mean": statistics.mean(launch_ms["unpack"]) if launch_ms["unpack"] else None,
+        "move_ms_mean": statistics.mean(launch_ms["move"]) if launch_ms["move"] else None,
+        "launches_per_step": len(durs) // args.steps,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "page_copy_kernel<8,false> (pack and unpack launches)",
+            "algorithmic_bytes_per_launch": int(statistics.mean(bytes_per_launch)),
+            "mean_launch_us": round(statistics.mean(durs) * 1e3, 2),
+        },
+    }
+    return res
+
+
+def verify(w, src, dst, s_ids, d_ids, dev) -> bool:
+    """Destination pages equal the source pages torch's own gather selects."""
+    import torch
+
+    for l in range(w.shape.num_layers):
+        a = src.layers[l].index_select(0, s_ids.long()).view(torch.int16)
+        b = dst.layers[l].index_select(0, d_ids.long()).view(torch.int16)
+        if not torch.equal(a, b):
+            return False
+    return True
+
+
+def run_promote(dev, steps=100, warmup=10):
+    """p50/p90 latency of promoting one 4096-token request."""
+    import torch
+
+    from paceserve_amd import workloads
+    from paceserve_amd.core.block_manager import BlockAllocator
+    from paceserve_amd.kv_transfer import migrate
+
+    w = workloads.config("promote4k")
+    src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev)
+    dst = workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev)
+    alloc = BlockAllocator(w.shape.page_size, w.dst_pool_pages)
+    mig = migrate.KVMigrator(src, dst, alloc)
+    host = torch.empty(w.payload_bytes, dtype=torch.uint8, pin_memory=True)
+    out = {}
+    for mode in ("buffer", "fused", "pinned"):
+        lat = []
+        n_iter = warmup + (steps if mode != "pinned" else max(20, steps // 5))
+        for i in range(n_iter):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            plan = mig.promote(w.src_tables, mode=mode, host_buf=host if mode == "pinned" else None)
+            ev = torch.cuda.Event()
+            ev.record()
+            ev.synchronize()
+            t1 = time.perf_counter()
+            for t in plan.dst_tables:             # return the pages (outside the timing)
+                alloc.free_many(reversed(t))
+            if i >= warmup:
+                lat.append((t1 - t0) * 1e6)
+        lat.sort()
+        out[mode] = {"p50_us": round(statistics.median(lat), 1),
+                     "p90_us": round(lat[int(0.9 * (len(lat) - 1))], 1), "runs": len(lat)}
+        log(f"promote4k {mode}: p50 {out[mode]['p50_us']} us")
+    out["payload_bytes"] = w.payload_bytes
+    return out
+
+
+def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan):
+    """The reference's CPU path on pageable host tensors: per layer,
+    index_select into the buffer then index_copy_ into the destination.  The
+    host pools are copies of the first layers of the device pools (same
+    bytes, same block tables)."""
+    import torch
+
+    from oracle import kv_oracle as orc
+
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    L = layers_sample
+    src = [t.cpu() for t in src_pool.layers[:L]]
+    dst = [t.cpu() for t in dst_pool.layers[:L]]
+    s_idx = torch.tensor(plan.src_ids, dtype=torch.long)
+    d_idx = torch.tensor(plan.dst_ids, dtype=torch.long)
+    buf = torch.empty((L, plan.n_pages) + w.shape.page_shape, dtype=w.shape.dtype)
+    orc.torch_cpu_pack_unpack(src, s_idx, dst, d_idx, buf)            # warm-up
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        orc.torch_cpu_pack_unpack(src, s_idx, dst, d_idx, buf)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    payload = L * plan.n_pages * w.shape.page_bytes
+    return {
+        "value": round(4 * payload / t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{L} of {w.shape.num_layers} layers, all {plan.n_pages} pages of {w.name} "
+                  f"({payload / 2**30:.2f} GiB payload), full-size pools per layer; median of 5 "
+                  f"after 1 warm-up; torch {torch.__version__} index_select/index_copy_ on host tensors",
+        "seconds_per_pass": round(t, 4),
+    }
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the KV migration path is measured on "
+                          "one device's share; --gpus N>1 is not supported"}), flush=True)
+        sys.exit(2)
+
+    import torch
+
+    from paceserve_amd import _native, workloads
+
+    _native.load()
+    dev = torch.device("cuda", 0)
+    w = workloads.config(args.workload)
+    log(f"workload {w.name}: {w.description}")
+    src, dst, plan, s_ids, d_ids = device_setup(w, dev)
+    res = run_device(args, w, dev, src, dst, plan, s_ids, d_ids)
+    log(f"device: {res['value']:.1f} GB/s ({res['value'] / HBM_PEAK_GBS * 100:.1f}% of peak), "
+        f"pack {res['pack_ms_mean']} ms, unpack {res['unpack_ms_mean']} ms")
+    if args.verify:
+        res["verified"] = verify(w, src, dst, s_ids, d_ids, dev)
+        log(f"verified: {res['verified']}")
+    cpu = None
+    if not args.no_cpu:
+        layers = args.cpu_layers or max(1, min(w.shape.num_layers, 8))
+        log(f"CPU baseline on {os.cpu_count()} cores, {layers} layers ...")
+        cpu = run_cpu_baseline(w, layers, src, dst, plan)
+        log(f"CPU baseline: {cpu['value']} GB/s")
+    del src, dst, s_ids, d_ids
+    torch.cuda.empty_cache()
+    promote = None
+    if not args.no_promote:
+        promote = run_promote(dev)
+
+    line = {
+        "metric": METRIC,
+        "value": round(res["value"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": str(w.shape.dtype).replace("torch.", ""),
+        "data": "synthetic (seeded N(0,1) pages generated on the GPU)",
+        "config": dict(w.summary(), mode=args.mode),
+        "pct_hbm_peak": round(res["value"] / HBM_PEAK_GBS * 100, 2),
+        "event_ms_per_step": round(res["event_ms_per_step"], 4),
+        "pack_ms": res["pack_ms_mean"],
+        "unpack_ms": res["unpack_ms_mean"],
+        "roofline": res["roofline"],
+        "promote_4k": promote,
+        "cpu_baseline": cpu,
+    }
+    if "verified" in res:
+        line["verified"] = res["verified"]
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

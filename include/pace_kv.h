@@ -1,0 +1,189 @@
+/*
+ * pace_kv.h — C ABI of the MI355X (gfx950) paged KV-cache migration library
+ * (libpace_kv.so).
+ *
+ * The path moves a request's paged KV cache out of one cache pool and into
+ * another.  Each pool is a list of L separately allocated per-layer device
+ * buffers, each laid out as [num_pages, 2, page_size, num_kv_heads, head_dim]
+ * (dim 1: 0 = K, 1 = V).  A "page" is one slice [2, page_size, H, D] of one
+ * layer: page_bytes = 2 * page_size * H * D * sizeof(elem) contiguous bytes.
+ * The library copies whole pages as raw bytes, so every dtype (fp16, bf16,
+ * fp8, fp32) is handled bit-exactly and the partial last page of a request is
+ * copied with all of its slots, stale ones included.
+ *
+ * Conventions
+ *  - Every entry point returns an int status: 0 (PACE_KV_OK) on success, a
+ *    negative PACE_KV_E* code for an argument error detected on the host, or a
+ *    positive hipError_t value from the HIP runtime.  pace_kv_last_error()
+ *    returns a message for the calling thread's last failure.
+ *  - Layer tables (src_layers / dst_layers) are HOST arrays of num_layers
+ *    DEVICE pointers.  Page-id arrays are DEVICE arrays of int32.
+ *  - All device pointers and page_bytes must be multiples of 16 bytes.
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and
+ *    the calls return without waiting for it.  The kernels never read or
+ *    write a page whose id lies outside [0, pool_pages): such a (layer, page)
+ *    tile is skipped and, when err_count (a device int32) is non-NULL, counted
+ *    there with an atomic add.
+ *  - Entry points are reentrant; none holds global locks or synchronises the
+ *    device.  A pace_kv_stager must be driven by one host thread at a time.
+ */
+#ifndef PACE_KV_H_
+#define PACE_KV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PACE_KV_ABI_VERSION 1
+
+/* Largest number of layers one kernel launch addresses; entry points split
+ * longer layer lists into several launches on the same stream. */
+#define PACE_KV_MAX_LAYERS_PER_LAUNCH 64
+
+enum pace_kv_status {
+  PACE_KV_OK = 0,
+  PACE_KV_EINVAL = -1,   /* null pointer, negative size, misalignment        */
+  PACE_KV_ERANGE = -2,   /* page id or size outside what a buffer holds      */
+  PACE_KV_ENOMEM = -3,   /* allocator exhausted (no free pages)              */
+  PACE_KV_ESTATE = -4    /* object used in a state that does not allow it    */
+};
+
+/* ABI version this library was built with (PACE_KV_ABI_VERSION). */
+int pace_kv_abi_version(void);
+
+/* Message describing the calling thread's most recent failing call. */
+const char* pace_kv_last_error(void);
+
+/* ------------------------------------------------------------------------ */
+/* Device-to-device page copies                                              */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * PACK (multi-layer gather).
+ *   out[l][j] = src_layers[l][page_ids[j]]   for l < num_layers, j < n_pages
+ * where out[l] = (char*)out + l * out_layer_stride and each element is one
+ * page of page_bytes.  Several requests are packed in one call by
+ * concatenating their block tables in page_ids (CSR order); request r's
+ * slice is then out[:, indptr[r]:indptr[r+1]].
+ *
+ * Replaces the per-layer gather in KVhelper.get_kv_cache
+ *   (paceserve/kv_transfer/kv_utils.py:44-46:
+ *    seq_cache[i] = gpu_cache[i][torch.tensor(kv_page_indices)]).
+ */
+int pace_kv_pack(const void* const* src_layers, int num_layers,
+                 int64_t pool_pages, const int32_t* page_ids, int64_t n_pages,
+                 int64_t page_bytes, void* out, int64_t out_layer_stride,
+                 int32_t* err_count, void* stream);
+
+/*
+ * UNPACK (multi-layer scatter through a remapped block table).
+ *   dst_layers[l][page_ids[j]] = buf[l][j]
+ * where buf[l] = (const char*)buf + l * buf_layer_stride.  Pages of the
+ * destination pools not named in page_ids are left untouched.  page_ids must
+ * not repeat a page (the host layer removes repeats, keeping the last
+ * occurrence, as a sequential index_put_ would).
+ *
+ * Replaces the per-layer scatter in KVhelper.insert_kv_cache
+ *   (paceserve/kv_transfer/kv_utils.py:49-52:
+ *    gpu_cache[i][torch.tensor(kv_indices)] = cached_content[i].to(device)).
+ */
+int pace_kv_unpack(const void* buf, int64_t buf_layer_stride,
+                   void* const* dst_layers, int num_layers, int64_t pool_pages,
+                   const int32_t* page_ids, int64_t n_pages, int64_t page_bytes,
+                   int32_t* err_count, void* stream);
+
+/*
+ * MOVE (pack and unpack fused, pool to pool on one device, no transfer buffer).
+ *   dst_layers[l][dst_ids[j]] = src_layers[l][src_ids[j]]
+ * Produces the same destination bytes as PACK followed by UNPACK with half of
+ * their HBM traffic.  Source and destination pages must not overlap.
+ *
+ * Replaces get_kv_cache followed by insert_kv_cache when both caches live on
+ * the same GPU (paceserve/worker/base_worker.py:236-281).
+ */
+int pace_kv_move(const void* const* src_layers, int64_t src_pool_pages,
+                 const int32_t* src_ids, void* const* dst_layers,
+                 int64_t dst_pool_pages, const int32_t* dst_ids,
+                 int num_layers, int64_t n_pages, int64_t page_bytes,
+                 int32_t* err_count, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Pinned-host staging (the host leg of a migration)                         */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * A stager owns two rings of device slots (one feeding device-to-host copies,
+ * one fed by host-to-device copies), two side streams (D2H and H2D, default
+ * priority) and the events that order them against the caller's stream.
+ * Each slot holds slot_bytes; a layer chunk of k layers needs
+ * k * n_pages * page_bytes <= slot_bytes.
+ */
+typedef struct pace_kv_stager pace_kv_stager;
+
+int pace_kv_stager_create(int64_t slot_bytes, int num_slots,
+                          pace_kv_stager** out);
+int pace_kv_stager_destroy(pace_kv_stager* stager);
+
+/*
+ * Pack into host memory: for every chunk of layers_per_chunk layers, PACK into
+ * a device slot on `stream`, then copy the slot to
+ * host_out + layer_begin * n_pages * page_bytes on the D2H side stream, so the
+ * copy of chunk c overlaps the pack of chunk c+1.  host_out receives the
+ * layout [num_layers, n_pages, page_size-slice...] of PACK with
+ * out_layer_stride = n_pages * page_bytes.  Pinned host memory gives
+ * asynchronous DMA; pageable memory works but the runtime stages it.
+ * When the call returns, `stream` is ordered after the last copy.
+ *
+ * Replaces the gather + pageable device-to-host copy loop of
+ * KVhelper.get_kv_cache (paceserve/kv_transfer/kv_utils.py:44-47).
+ */
+int pace_kv_pack_to_host(pace_kv_stager* stager,
+                         const void* const* src_layers, int num_layers,
+                         int64_t pool_pages, const int32_t* page_ids,
+                         int64_t n_pages, int64_t page_bytes,
+                         int layers_per_chunk, void* host_out,
+                         int32_t* err_count, void* stream);
+
+/*
+ * Unpack from host memory: the mirror of pace_kv_pack_to_host.  Chunk c is
+ * copied host-to-device on the H2D side stream while chunk c-1 is unpacked on
+ * `stream`.
+ *
+ * Replaces the pageable host-to-device copy + scatter loop of
+ * KVhelper.insert_kv_cache (paceserve/kv_transfer/kv_utils.py:49-52).
+ */
+int pace_kv_unpack_from_host(pace_kv_stager* stager, const void* host_in,
+                             void* const* dst_layers, int num_layers,
+                             int64_t pool_pages, const int32_t* page_ids,
+                             int64_t n_pages, int64_t page_bytes,
+                             int layers_per_chunk, int32_t* err_count,
+                             void* stream);
+
+/*
+ * Full host round trip in one pipeline: pack(c) -> D2H(c) -> H2D(c) ->
+ * unpack(c) per layer chunk, with pack(c+1), D2H(c), H2D(c-1) and
+ * unpack(c-2) in flight together (D2H and H2D use separate DMA queues).
+ * host_buf holds host_bytes of host memory used as a ring of chunk-sized
+ * regions (host_bytes >= one chunk; pass the full payload to keep a complete
+ * host copy, as the reference's KVobj does).
+ *
+ * Replaces KVhelper.get_kv_cache followed by KVhelper.insert_kv_cache through
+ * host DRAM (paceserve/worker/base_worker.py:236-281,
+ * paceserve/engine/decode_llm_engine.py:31-41).
+ */
+int pace_kv_roundtrip(pace_kv_stager* stager,
+                      const void* const* src_layers, int64_t src_pool_pages,
+                      const int32_t* src_ids, void* const* dst_layers,
+                      int64_t dst_pool_pages, const int32_t* dst_ids,
+                      int num_layers, int64_t n_pages, int64_t page_bytes,
+                      int layers_per_chunk, void* host_buf, int64_t host_bytes,
+                      int32_t* err_count, void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* PACE_KV_H_ */

@@ -1,0 +1,69 @@
+"""Builds libpace_kv.so (the HIP kernels and their C ABI) in-tree for gfx950.
+
+Usage: ``python -m paceserve_amd.build``.  The library is written next to this
+file so that it travels with the source tree; ``paceserve_amd._native`` loads
+it from there and never builds on import.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_DIR = PKG_DIR.parent
+CSRC_DIR = PKG_DIR / "csrc"
+INCLUDE_DIR = REPO_DIR / "include"
+LIB_NAME = "libpace_kv.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+
+SOURCES = ["kv_copy.hip", "kv_stage.hip"]
+HEADERS = ["internal.h"]
+
+# Packed-FP32 instructions are disabled for every HIP translation unit.
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-Wall",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def hipcc_path() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cand = Path(rocm) / "bin" / "hipcc"
+    if cand.exists():
+        return str(cand)
+    found = shutil.which("hipcc")
+    if not found:
+        raise RuntimeError("hipcc not found (set ROCM_PATH)")
+    return found
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compiles every HIP source into LIB_PATH (always recompiles)."""
+    srcs = [str(CSRC_DIR / s) for s in SOURCES]
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc_path(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}", "-o", str(tmp), *srcs]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature.
+    noise = "packed-fp32-ops"
+    msgs = [ln for ln in (proc.stdout + proc.stderr).splitlines() if noise not in ln]
+    if proc.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
+    if verbose and msgs:
+        print("\n".join(msgs), flush=True)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    path = build_library(verbose="-v" in sys.argv)
+    print(path)

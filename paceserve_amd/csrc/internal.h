@@ -1,0 +1,39 @@
+// Shared declarations between the translation units of libpace_kv.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pace_kv.h"
+
+namespace pace_kv {
+
+// Records `msg` (printf-style) as the calling thread's last error and returns
+// `code`, so call sites read `return fail(PACE_KV_EINVAL, "...")`.
+int fail(int code, const char* fmt, ...);
+
+// Converts a HIP error into the ABI's status convention (positive hipError_t)
+// and records its message; returns 0 for hipSuccess.
+int hip_status(hipError_t err, const char* what);
+
+// One side of a page copy: per-layer base pointers plus an optional device
+// page-id array (NULL means page j of layer l is at base[l] + j*page_bytes,
+// which is how the contiguous transfer buffer is addressed).
+struct Side {
+  const char* const* layers;  // host array, num_layers entries
+  const int32_t* ids;         // device array of n_pages ids, or nullptr
+  int64_t pool_pages;         // ids must lie in [0, pool_pages)
+};
+
+// Validates arguments and enqueues the copy dst[l][dst_id(j)] = src[l][src_id(j)]
+// for l < num_layers, j < n_pages on `stream`, in launches of at most
+// PACE_KV_MAX_LAYERS_PER_LAUNCH layers.
+int launch_page_copy(const Side& src, const Side& dst, int num_layers,
+                     int64_t n_pages, int64_t page_bytes, int32_t* err_count,
+                     hipStream_t stream);
+
+// Builds the layer table of a contiguous buffer [num_layers][layer_stride].
+void buffer_layers(const void* base, int64_t layer_stride, int num_layers,
+                   const char** out);
+
+}  // namespace pace_kv

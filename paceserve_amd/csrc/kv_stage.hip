@@ -1,0 +1,310 @@
+// Pinned-host staging of packed KV pages: the host leg of a migration.
+//
+// A migration through host DRAM moves every payload byte over PCIe twice
+// (device->host, host->device), at <= ~64 GB/s per direction, i.e. two orders
+// of magnitude slower than the on-device pack/unpack.  The pipeline therefore
+// aims to keep both DMA directions busy at once and to hide pack/unpack under
+// them: layers are processed in chunks, and with three streams
+//   caller stream : pack(c) ........ unpack(c-2)
+//   D2H stream    :        D2H(c)
+//   H2D stream    :               H2D(c-1)
+// chunk c's device-to-host copy overlaps chunk c-1's host-to-device copy (the
+// two directions use separate DMA engines) and the kernels of neighbouring
+// chunks.  Events carry every dependency; nothing blocks the host.
+//
+// Device slots are reused round-robin; before a slot is overwritten, the
+// stream that writes it waits for the event recorded after the last read of
+// that slot, so back-to-back calls on one stager are ordered correctly.
+#include <string.h>
+
+#include <vector>
+
+#include "internal.h"
+
+using pace_kv::fail;
+using pace_kv::hip_status;
+
+struct pace_kv_stager {
+  int device = -1;
+  int64_t slot_bytes = 0;
+  int num_slots = 0;
+  char* out_ring = nullptr;  // num_slots device slots written by pack, read by D2H
+  char* in_ring = nullptr;   // num_slots device slots written by H2D, read by unpack
+  hipStream_t d2h = nullptr;
+  hipStream_t h2d = nullptr;
+  hipEvent_t start = nullptr;
+  hipEvent_t d2h_done = nullptr;
+  std::vector<hipEvent_t> packed;    // out slot s filled (caller stream)
+  std::vector<hipEvent_t> out_free;  // out slot s drained by D2H (D2H stream)
+  std::vector<hipEvent_t> in_ready;  // in slot s filled by H2D (H2D stream)
+  std::vector<hipEvent_t> in_free;   // in slot s drained by unpack (caller stream)
+  std::vector<hipEvent_t> host_full;  // host region r written by D2H
+  std::vector<hipEvent_t> host_free;  // host region r read by H2D
+};
+
+namespace {
+
+hipError_t make_events(std::vector<hipEvent_t>& v, size_t n) {
+  while (v.size() < n) {
+    hipEvent_t e;
+    hipError_t err = hipEventCreateWithFlags(&e, hipEventDisableTiming);
+    if (err != hipSuccess) return err;
+    v.push_back(e);
+  }
+  return hipSuccess;
+}
+
+void destroy_events(std::vector<hipEvent_t>& v) {
+  for (hipEvent_t e : v) (void)hipEventDestroy(e);
+  v.clear();
+}
+
+void release(pace_kv_stager* s) {
+  if (s->out_ring) (void)hipFree(s->out_ring);
+  if (s->in_ring) (void)hipFree(s->in_ring);
+  if (s->d2h) (void)hipStreamDestroy(s->d2h);
+  if (s->h2d) (void)hipStreamDestroy(s->h2d);
+  if (s->start) (void)hipEventDestroy(s->start);
+  if (s->d2h_done) (void)hipEventDestroy(s->d2h_done);
+  destroy_events(s->packed);
+  destroy_events(s->out_free);
+  destroy_events(s->in_ready);
+  destroy_events(s->in_free);
+  destroy_events(s->host_full);
+  destroy_events(s->host_free);
+  delete s;
+}
+
+int check_stager(pace_kv_stager* s) {
+  if (s == nullptr) return fail(PACE_KV_EINVAL, "stager is NULL");
+  int dev = -1;
+  int rc = hip_status(hipGetDevice(&dev), "hipGetDevice");
+  if (rc) return rc;
+  if (dev != s->device)
+    return fail(PACE_KV_ESTATE, "stager belongs to device %d but device %d is current", s->device, dev);
+  return PACE_KV_OK;
+}
+
+struct ChunkPlan {
+  int num_layers;
+  int layers_per_chunk;
+  int64_t n_pages;
+  int64_t page_bytes;
+  int64_t layer_bytes;  // n_pages * page_bytes
+  int num_chunks() const { return (num_layers + layers_per_chunk - 1) / layers_per_chunk; }
+  int first(int c) const { return c * layers_per_chunk; }
+  int count(int c) const {
+    const int rest = num_layers - first(c);
+    return rest < layers_per_chunk ? rest : layers_per_chunk;
+  }
+};
+
+int make_plan(const pace_kv_stager* s, int num_layers, int64_t n_pages, int64_t page_bytes,
+              int layers_per_chunk, ChunkPlan* plan) {
+  if (num_layers < 0 || n_pages < 0) return fail(PACE_KV_EINVAL, "negative num_layers or n_pages");
+  if (page_bytes <= 0 || page_bytes % 16 != 0)
+    return fail(PACE_KV_EINVAL, "page_bytes must be a positive multiple of 16");
+  if (layers_per_chunk <= 0) return fail(PACE_KV_EINVAL, "layers_per_chunk must be >= 1");
+  if (n_pages > INT64_MAX / page_bytes) return fail(PACE_KV_ERANGE, "payload size overflows");
+  plan->num_layers = num_layers;
+  plan->layers_per_chunk = layers_per_chunk < num_layers ? layers_per_chunk : (num_layers > 0 ? num_layers : 1);
+  plan->n_pages = n_pages;
+  plan->page_bytes = page_bytes;
+  plan->layer_bytes = n_pages * page_bytes;
+  if (plan->layer_bytes > 0 && int64_t(plan->layers_per_chunk) > s->slot_bytes / plan->layer_bytes)
+    return fail(PACE_KV_ERANGE,
+                "a chunk of %d layers needs %lld bytes but a stager slot holds %lld",
+                plan->layers_per_chunk, (long long)(plan->layer_bytes * plan->layers_per_chunk),
+                (long long)s->slot_bytes);
+  return PACE_KV_OK;
+}
+
+#define PACE_TRY(expr)      \
+  do {                      \
+    int rc_ = (expr);       \
+    if (rc_) return rc_;    \
+  } while (0)
+
+#define PACE_HIP(expr, what) PACE_TRY(hip_status((expr), (what)))
+
+// pack(chunk c) of the source pool into out slot `slot`, on `stream`.
+int pack_chunk(pace_kv_stager* s, const ChunkPlan& p, int c, const void* const* src_layers,
+               int64_t pool_pages, const int32_t* ids, int32_t* err, hipStream_t stream) {
+  char* slot = s->out_ring + (c % s->num_slots) * s->slot_bytes;
+  return pace_kv_pack(src_layers + p.first(c), p.count(c), pool_pages, ids, p.n_pages,
+                      p.page_bytes, slot, p.layer_bytes, err, stream);
+}
+
+int unpack_chunk(pace_kv_stager* s, const ChunkPlan& p, int c, void* const* dst_layers,
+                 int64_t pool_pages, const int32_t* ids, int32_t* err, hipStream_t stream) {
+  const char* slot = s->in_ring + (c % s->num_slots) * s->slot_bytes;
+  return pace_kv_unpack(slot, p.layer_bytes, dst_layers + p.first(c), p.count(c), pool_pages, ids,
+                        p.n_pages, p.page_bytes, err, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int pace_kv_stager_create(int64_t slot_bytes, int num_slots, pace_kv_stager** out) {
+  if (out == nullptr) return fail(PACE_KV_EINVAL, "stager_create: out is NULL");
+  *out = nullptr;
+  if (slot_bytes <= 0 || slot_bytes % 256 != 0)
+    return fail(PACE_KV_EINVAL, "slot_bytes must be a positive multiple of 256");
+  if (num_slots < 2 || num_slots > 64) return fail(PACE_KV_EINVAL, "num_slots must be in [2, 64]");
+  pace_kv_stager* s = new pace_kv_stager();
+  s->slot_bytes = slot_bytes;
+  s->num_slots = num_slots;
+  hipError_t e = hipGetDevice(&s->device);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&s->out_ring), slot_bytes * num_slots);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&s->in_ring), slot_bytes * num_slots);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->d2h, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->h2d, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&s->start, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&s->d2h_done, hipEventDisableTiming);
+  if (e == hipSuccess) e = make_events(s->packed, num_slots);
+  if (e == hipSuccess) e = make_events(s->out_free, num_slots);
+  if (e == hipSuccess) e = make_events(s->in_ready, num_slots);
+  if (e == hipSuccess) e = make_events(s->in_free, num_slots);
+  if (e != hipSuccess) {
+    int rc = hip_status(e, "stager_create");
+    release(s);
+    return rc;
+  }
+  *out = s;
+  return PACE_KV_OK;
+}
+
+int pace_kv_stager_destroy(pace_kv_stager* s) {
+  if (s == nullptr) return PACE_KV_OK;
+  // Work enqueued through the stager may still use its slots and streams.
+  hipError_t e1 = hipStreamSynchronize(s->d2h);
+  hipError_t e2 = hipStreamSynchronize(s->h2d);
+  for (hipEvent_t e : s->in_free) (void)hipEventSynchronize(e);
+  release(s);
+  if (e1 != hipSuccess) return hip_status(e1, "stager_destroy (D2H stream)");
+  return hip_status(e2, "stager_destroy (H2D stream)");
+}
+
+int pace_kv_pack_to_host(pace_kv_stager* s, const void* const* src_layers, int num_layers,
+                         int64_t pool_pages, const int32_t* page_ids, int64_t n_pages,
+                         int64_t page_bytes, int layers_per_chunk, void* host_out,
+                         int32_t* err_count, void* stream_) {
+  PACE_TRY(check_stager(s));
+  ChunkPlan p;
+  PACE_TRY(make_plan(s, num_layers, n_pages, page_bytes, layers_per_chunk, &p));
+  if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
+  if (host_out == nullptr) return fail(PACE_KV_EINVAL, "pack_to_host: host_out is NULL");
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  for (int c = 0; c < p.num_chunks(); ++c) {
+    const int slot = c % s->num_slots;
+    PACE_HIP(hipStreamWaitEvent(stream, s->out_free[slot], 0), "wait out slot");
+    PACE_TRY(pack_chunk(s, p, c, src_layers, pool_pages, page_ids, err_count, stream));
+    PACE_HIP(hipEventRecord(s->packed[slot], stream), "record packed");
+    PACE_HIP(hipStreamWaitEvent(s->d2h, s->packed[slot], 0), "wait packed");
+    PACE_HIP(hipMemcpyAsync(static_cast<char*>(host_out) + p.first(c) * p.layer_bytes,
+                            s->out_ring + slot * s->slot_bytes, p.count(c) * p.layer_bytes,
+                            hipMemcpyDeviceToHost, s->d2h),
+             "D2H copy");
+    PACE_HIP(hipEventRecord(s->out_free[slot], s->d2h), "record out_free");
+  }
+  PACE_HIP(hipEventRecord(s->d2h_done, s->d2h), "record d2h_done");
+  PACE_HIP(hipStreamWaitEvent(stream, s->d2h_done, 0), "join D2H");
+  return PACE_KV_OK;
+}
+
+int pace_kv_unpack_from_host(pace_kv_stager* s, const void* host_in, void* const* dst_layers,
+                             int num_layers, int64_t pool_pages, const int32_t* page_ids,
+                             int64_t n_pages, int64_t page_bytes, int layers_per_chunk,
+                             int32_t* err_count, void* stream_) {
+  PACE_TRY(check_stager(s));
+  ChunkPlan p;
+  PACE_TRY(make_plan(s, num_layers, n_pages, page_bytes, layers_per_chunk, &p));
+  if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
+  if (host_in == nullptr) return fail(PACE_KV_EINVAL, "unpack_from_host: host_in is NULL");
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  // The caller's earlier work (e.g. writes of host_in by a kernel) comes first.
+  PACE_HIP(hipEventRecord(s->start, stream), "record start");
+  PACE_HIP(hipStreamWaitEvent(s->h2d, s->start, 0), "wait start");
+  for (int c = 0; c < p.num_chunks(); ++c) {
+    const int slot = c % s->num_slots;
+    PACE_HIP(hipStreamWaitEvent(s->h2d, s->in_free[slot], 0), "wait in slot");
+    PACE_HIP(hipMemcpyAsync(s->in_ring + slot * s->slot_bytes,
+                            static_cast<const char*>(host_in) + p.first(c) * p.layer_bytes,
+                            p.count(c) * p.layer_bytes, hipMemcpyHostToDevice, s->h2d),
+             "H2D copy");
+    PACE_HIP(hipEventRecord(s->in_ready[slot], s->h2d), "record in_ready");
+    PACE_HIP(hipStreamWaitEvent(stream, s->in_ready[slot], 0), "wait in_ready");
+    PACE_TRY(unpack_chunk(s, p, c, dst_layers, pool_pages, page_ids, err_count, stream));
+    PACE_HIP(hipEventRecord(s->in_free[slot], stream), "record in_free");
+  }
+  return PACE_KV_OK;
+}
+
+int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t src_pool_pages,
+                      const int32_t* src_ids, void* const* dst_layers, int64_t dst_pool_pages,
+                      const int32_t* dst_ids, int num_layers, int64_t n_pages, int64_t page_bytes,
+                      int layers_per_chunk, void* host_buf, int64_t host_bytes,
+                      int32_t* err_count, void* stream_) {
+  PACE_TRY(check_stager(s));
+  ChunkPlan p;
+  PACE_TRY(make_plan(s, num_layers, n_pages, page_bytes, layers_per_chunk, &p));
+  if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
+  if (host_buf == nullptr) return fail(PACE_KV_EINVAL, "roundtrip: host_buf is NULL");
+  const int64_t chunk_bytes = p.layer_bytes * p.layers_per_chunk;
+  if (host_bytes < chunk_bytes)
+    return fail(PACE_KV_ERANGE, "roundtrip: host buffer (%lld bytes) is smaller than one chunk (%lld)",
+                (long long)host_bytes, (long long)chunk_bytes);
+  const int chunks = p.num_chunks();
+  int64_t regions64 = host_bytes / chunk_bytes;
+  const int regions = regions64 < chunks ? static_cast<int>(regions64) : chunks;
+  PACE_HIP(make_events(s->host_full, regions), "create host events");
+  PACE_HIP(make_events(s->host_free, regions), "create host events");
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  char* host = static_cast<char*>(host_buf);
+  PACE_HIP(hipEventRecord(s->start, stream), "record start");
+  PACE_HIP(hipStreamWaitEvent(s->h2d, s->start, 0), "wait start");
+  // unpack(c) is issued on the caller stream after pack(c + kLag), so that the
+  // stream's wait for H2D(c) does not hold back the packs that feed the D2H
+  // queue.
+  const int kLag = 2;
+  int next_unpack = 0;
+  auto issue_unpack = [&](int c) -> int {
+    const int slot = c % s->num_slots;
+    PACE_HIP(hipStreamWaitEvent(stream, s->in_ready[slot], 0), "wait in_ready");
+    PACE_TRY(unpack_chunk(s, p, c, dst_layers, dst_pool_pages, dst_ids, err_count, stream));
+    PACE_HIP(hipEventRecord(s->in_free[slot], stream), "record in_free");
+    return PACE_KV_OK;
+  };
+  for (int c = 0; c < chunks; ++c) {
+    const int slot = c % s->num_slots;
+    const int r = c % regions;
+    char* region = host + static_cast<int64_t>(r) * chunk_bytes;
+    const int64_t bytes = p.count(c) * p.layer_bytes;
+    PACE_HIP(hipStreamWaitEvent(stream, s->out_free[slot], 0), "wait out slot");
+    PACE_TRY(pack_chunk(s, p, c, src_layers, src_pool_pages, src_ids, err_count, stream));
+    PACE_HIP(hipEventRecord(s->packed[slot], stream), "record packed");
+    PACE_HIP(hipStreamWaitEvent(s->d2h, s->packed[slot], 0), "wait packed");
+    PACE_HIP(hipStreamWaitEvent(s->d2h, s->host_free[r], 0), "wait host region");
+    PACE_HIP(hipMemcpyAsync(region, s->out_ring + slot * s->slot_bytes, bytes,
+                            hipMemcpyDeviceToHost, s->d2h),
+             "D2H copy");
+    PACE_HIP(hipEventRecord(s->out_free[slot], s->d2h), "record out_free");
+    PACE_HIP(hipEventRecord(s->host_full[r], s->d2h), "record host_full");
+    // unpack(c - kLag) last reads in slot (c - kLag) % num_slots; it must be
+    // enqueued before H2D(c) waits on in_free of slot c % num_slots, which is
+    // the same slot when num_slots == kLag.
+    if (c - kLag >= next_unpack) PACE_TRY(issue_unpack(next_unpack++));
+    PACE_HIP(hipStreamWaitEvent(s->h2d, s->host_full[r], 0), "wait host_full");
+    PACE_HIP(hipStreamWaitEvent(s->h2d, s->in_free[slot], 0), "wait in slot");
+    PACE_HIP(hipMemcpyAsync(s->in_ring + slot * s->slot_bytes, region, bytes,
+                            hipMemcpyHostToDevice, s->h2d),
+             "H2D copy");
+    PACE_HIP(hipEventRecord(s->in_ready[slot], s->h2d), "record in_ready");
+    PACE_HIP(hipEventRecord(s->host_free[r], s->h2d), "record host_free");
+  }
+  while (next_unpack < chunks) PACE_TRY(issue_unpack(next_unpack++));
+  return PACE_KV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,212 @@
+"""KVhelper: drop-in for paceserve.kv_transfer.kv_utils.KVhelper
+(paceserve/kv_transfer/kv_utils.py:8-56) with its page movement in HIP.
+
+Same constructor, methods, return values and error behaviour:
+  - __init__ reads only get_num_q_heads / get_num_kv_heads(parallel_config),
+    get_head_size(), dtype, get_num_layers(parallel_config) and
+    cache_config.block_size (kv_utils.py:10-24);
+  - get_kv_cache(seq, seq_manager) -> (host tensor [L, n, 2, P, H, D], ids),
+    or (zeros [L, 1, ...], [0]) when the sequence has no block table
+    (kv_utils.py:33-47); out-of-range ids raise IndexError as torch indexing does;
+  - insert_kv_cache(cached_content, kv_indices, device) -> bool, never raises:
+    any error prints "error during insert kv cache: ..." and returns False
+    (kv_utils.py:49-56);
+  - reset_kv_cache(num_gpu_blocks) replaces every layer with a zero tensor
+    (kv_utils.py:29-31).
+
+What changes underneath: the reference gathers each layer with torch
+advanced indexing into a temporary device tensor and copies it to *pageable*
+host memory synchronously, L times; here one kernel per layer chunk packs the
+pages into a device slot while the previous chunk streams to *pinned* host
+memory on a side stream (pace_kv_pack_to_host), and insert is the mirror
+(pace_kv_unpack_from_host).  Device-resident transfer buffers skip the host
+leg (pack_pages / unpack_pages).
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import ops
+
+# Target bytes of one staged layer chunk: large enough for full-rate DMA,
+# small enough that several chunks overlap for a mid-sized request.
+STAGE_CHUNK_BYTES = 64 << 20
+STAGE_MIN_CHUNKS = 4
+STAGE_SLOTS = 3
+
+
+def normalize_page_ids(ids: Sequence[int], num_pages: int) -> List[int]:
+    """torch advanced-indexing semantics for a list of page ids: negative ids
+    count from the end, anything outside [-num_pages, num_pages) raises
+    IndexError."""
+    out = []
+    for i in ids:
+        i = int(i)
+        if i < -num_pages or i >= num_pages:
+            raise IndexError(f"index {i} is out of bounds for dimension 0 with size {num_pages}")
+        out.append(i + num_pages if i < 0 else i)
+    return out
+
+
+def dedup_keep_last(ids: List[int]) -> List[int]:
+    """Positions of `ids` that survive when repeated pages are written in
+    order (the last write wins, as in a sequential index_put_)."""
+    last = {}
+    for pos, pid in enumerate(ids):
+        last[pid] = pos
+    return sorted(last.values())
+
+
+def chunk_layers(num_layers: int, layer_bytes: int) -> int:
+    """Layers per staged chunk for a request of layer_bytes per layer."""
+    if layer_bytes <= 0:
+        return max(1, num_layers)
+    by_size = max(1, STAGE_CHUNK_BYTES // layer_bytes)
+    by_count = max(1, -(-num_layers // STAGE_MIN_CHUNKS))
+    return max(1, min(num_layers, by_size, by_count))
+
+
+class KVhelper:
+    def __init__(self, rank: int, model_config, cache_config, parallel_config):
+        self.rank = rank
+        self.num_q_heads = model_config.get_num_q_heads(parallel_config)
+        self.num_kv_heads = model_config.get_num_kv_heads(parallel_config)
+        self.head_dim = model_config.get_head_size()
+        self.dtype = model_config.dtype
+        self.block_size = cache_config.block_size
+        self.num_layers = model_config.get_num_layers(parallel_config)
+        self.model_runner = None
+        self._pool: Optional[ops.PagedPool] = None
+        self._stager: Optional[ops.Stager] = None
+        print(f"kv helper initialized on worker: {self.rank}")
+
+    # ---------------------------------------------------------------- pools
+
+    def add_model_runner(self, model_runner) -> None:
+        self.model_runner = model_runner
+
+    def _gpu_cache(self) -> List[torch.Tensor]:
+        return self.model_runner.attention_backend_wrapper.gpu_cache
+
+    def pool(self) -> ops.PagedPool:
+        """The bound cache as a PagedPool (rebuilt when its tensors change)."""
+        cache = self._gpu_cache()
+        if self._pool is None or not self._pool.holds(cache):
+            self._pool = ops.PagedPool(cache[: self.num_layers])
+        return self._pool
+
+    def _stager_for(self, pool: ops.PagedPool, slot_bytes: int) -> ops.Stager:
+        st = self._stager
+        if st is not None and (st.slot_bytes < slot_bytes or st.device != pool.device):
+            torch.cuda.current_stream(st.device).synchronize()
+            st.close()
+            st = None
+        if st is None:
+            st = ops.Stager(-(-slot_bytes // 256) * 256, STAGE_SLOTS, pool.device)
+            self._stager = st
+        return st
+
+    def page_shape(self):
+        return (2, self.block_size, self.num_kv_heads, self.head_dim)
+
+    def reset_kv_cache(self, num_gpu_blocks: int) -> None:
+        cache = self._gpu_cache()
+        for i in range(self.num_layers):
+            cache[i] = torch.zeros(num_gpu_blocks, *self.page_shape(), dtype=self.dtype, device="cuda")
+        self._pool = None
+
+    # ------------------------------------------------------- reference API
+
+    def get_kv_cache(self, seq, seq_manager):
+        try:
+            kv_page_indices = seq_manager._get_block_table(seq)
+        except Exception:
+            print(f"seq {seq.seq_id} was not allocated any memory")
+            kv_page_indices = None
+
+        if not kv_page_indices:
+            return torch.zeros(self.num_layers, 1, *self.page_shape(), dtype=self.dtype), [0]
+
+        pool = self.pool()
+        ids = normalize_page_ids(kv_page_indices, pool.num_pages)
+        n = len(ids)
+        host = torch.empty((self.num_layers, n) + pool.page_shape, dtype=pool.dtype, pin_memory=True)
+        layer_bytes = n * pool.page_bytes
+        k = chunk_layers(self.num_layers, layer_bytes)
+        with torch.cuda.device(pool.device):
+            stager = self._stager_for(pool, k * layer_bytes)
+            stager.pack_to_host(pool, ids, host, k)
+            torch.cuda.current_stream(pool.device).synchronize()
+        return host, kv_page_indices
+
+    def insert_kv_cache(self, cached_content, kv_indices, device) -> bool:
+        try:
+            self._insert(cached_content, kv_indices, device)
+            return True
+        except Exception as e:  # the reference's convention: report, never raise
+            print(f"error during insert kv cache: {e}")
+            return False
+
+    # ------------------------------------------------------ additive API
+
+    def pack_pages(self, page_ids, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Device-resident pack of this cache's pages: [L, n, 2, P, H, D]."""
+        pool = self.pool()
+        ids = normalize_page_ids(page_ids, pool.num_pages)
+        return ops.pack(pool, ids, out)
+
+    def unpack_pages(self, buf: torch.Tensor, page_ids) -> None:
+        """Device-resident unpack into this cache (ids must be distinct)."""
+        pool = self.pool()
+        ids = normalize_page_ids(page_ids, pool.num_pages)
+        if len(set(ids)) != len(ids):
+            raise ValueError("destination page ids repeat a page")
+        ops.unpack(buf, pool, ids)
+
+    # ------------------------------------------------------------ internals
+
+    def _insert(self, cached_content, kv_indices, device) -> None:
+        dev = torch.device(device) if not isinstance(device, int) else torch.device("cuda", device)
+        if dev.type != "cuda":
+            raise RuntimeError(f"cannot insert into a device cache from device {dev}")
+        ids_in = list(kv_indices)
+        if not ids_in:
+            # torch.tensor([]) is a float tensor, which cannot index.
+            raise IndexError("tensors used as indices must be long, int, byte or bool tensors")
+        pool = self.pool()
+        ids = normalize_page_ids(ids_in, pool.num_pages)
+        if not isinstance(cached_content, torch.Tensor):
+            raise TypeError("cached_content must be a tensor")
+        if cached_content.dim() != 2 + len(pool.page_shape) or cached_content.shape[0] < self.num_layers:
+            raise IndexError(f"cached_content of shape {tuple(cached_content.shape)} does not hold "
+                             f"{self.num_layers} layers of pages {pool.page_shape}")
+        if tuple(cached_content.shape[2:]) != pool.page_shape:
+            raise RuntimeError(f"page shape {tuple(cached_content.shape[2:])} != cache page shape {pool.page_shape}")
+        if cached_content.dtype != pool.dtype:
+            raise RuntimeError(f"Index put requires the source and destination dtypes match, "
+                               f"got {pool.dtype} for the destination and {cached_content.dtype} for the source.")
+        content = cached_content[: self.num_layers]
+        n = content.shape[1]
+        if n != len(ids):
+            if n != 1:
+                raise RuntimeError(f"shape mismatch: value tensor of shape {tuple(content.shape[1:])} "
+                                   f"cannot be broadcast to indexing result of shape "
+                                   f"{(len(ids),) + pool.page_shape}")
+            content = content.expand((self.num_layers, len(ids)) + pool.page_shape)
+        keep = dedup_keep_last(ids)
+        if len(keep) != len(ids):
+            ids = [ids[p] for p in keep]
+            content = content[:, keep]
+        with torch.cuda.device(pool.device):
+            stream = torch.cuda.current_stream(pool.device)
+            if content.device.type == "cuda":
+                ops.unpack(content.contiguous(), pool, ids)
+            else:
+                content = content.contiguous()
+                layer_bytes = len(ids) * pool.page_bytes
+                k = chunk_layers(self.num_layers, layer_bytes)
+                stager = self._stager_for(pool, k * layer_bytes)
+                stager.unpack_from_host(content, pool, ids, k)
+            stream.synchronize()

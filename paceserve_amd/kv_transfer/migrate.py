@@ -1,0 +1,163 @@
+"""Batched promotion: move whole requests from a source pool to a destination
+pool on one GPU (the additive batch API over the reference's per-request
+get_kv_cache / _insert_kv_cache pair, paceserve/worker/base_worker.py:236-281).
+
+One promote() call:
+  1. allocates every request's destination pages from the destination's LIFO
+     allocator, request by request, as BaseWorker._insert_kv_cache does
+     (base_worker.py:255-262), all-or-nothing for the batch;
+  2. remaps positionally, dropping a trailing extra destination page (the n vs
+     n+1 rule, base_worker.py:264-277);
+  3. uploads both id lists (CSR-concatenated over requests) with one pinned
+     host-to-device copy;
+  4. moves the pages in one of three modes:
+       "buffer": pack into a device transfer buffer, then unpack - the
+                 reference's two-step semantics, with the buffer as the
+                 device-resident KVobj payload; layer-chunked when the
+                 buffer would be large;
+       "fused":  pool-to-pool move, no buffer (half the HBM traffic);
+       "pinned": the full device->host->device round trip through pinned
+                 memory, overlapped per layer chunk (pace_kv_roundtrip).
+Each request's slice of the transfer buffer, buf[:, indptr[r]:indptr[r+1]],
+is byte-identical to what the reference's get_kv_cache returns for it.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
+
+import torch
+
+from ..core.block_manager import BlockAllocator, remap_dst_table
+from . import ops
+from .kv_utils import normalize_page_ids
+
+
+@dataclass
+class MigrationPlan:
+    src_ids: List[int]          # concatenated source pages (CSR over requests)
+    dst_ids: List[int]          # concatenated destination pages written
+    dst_tables: List[List[int]]  # full destination block tables (incl. any +1 page)
+    indptr: List[int]           # request r owns positions [indptr[r], indptr[r+1])
+
+    @property
+    def n_pages(self) -> int:
+        return len(self.src_ids)
+
+
+def plan_batch(src_tables: Sequence[Sequence[int]], src_num_pages: int, dst_allocator: BlockAllocator,
+               dst_pages: Optional[Sequence[int]] = None) -> MigrationPlan:
+    """Allocates destination pages for a batch of requests and remaps them.
+
+    Request r gets dst_pages[r] pages (default len(src_tables[r])) popped from
+    dst_allocator in request order; its source pages land positionally in the
+    first len(src_tables[r]) of them (an extra trailing page stays untouched).
+    Raises ValueError, allocating nothing, if a count is neither n nor n+1 or
+    the destination cannot hold the batch; IndexError for a source id outside
+    the source pool."""
+    if dst_pages is None:
+        dst_pages = [len(t) for t in src_tables]
+    if len(dst_pages) != len(src_tables):
+        raise ValueError("one destination page count per request")
+    src_ids: List[int] = []
+    indptr = [0]
+    for t in src_tables:
+        src_ids.extend(normalize_page_ids(t, src_num_pages))
+        indptr.append(len(src_ids))
+    for r, (t, m) in enumerate(zip(src_tables, dst_pages)):
+        if remap_dst_table([0] * m, len(t)) is None:
+            raise ValueError(f"request {r}: {m} destination pages cannot receive {len(t)} pages")
+    pages = dst_allocator.allocate_many(sum(dst_pages))
+    dst_tables: List[List[int]] = []
+    dst_ids: List[int] = []
+    pos = 0
+    for t, m in zip(src_tables, dst_pages):
+        table = pages[pos:pos + m]
+        pos += m
+        dst_tables.append(table)
+        dst_ids.extend(remap_dst_table(table, len(t)))
+    return MigrationPlan(src_ids, dst_ids, dst_tables, indptr)
+
+
+class KVMigrator:
+    def __init__(self, src, dst, dst_allocator: BlockAllocator, *,
+                 buffer_bytes_max: int = 8 << 30, stager: Optional[ops.Stager] = None):
+        self.src = ops.as_pool(src)
+        self.dst = ops.as_pool(dst)
+        if not self.src.compatible(self.dst) or self.src.num_layers != self.dst.num_layers:
+            raise ValueError("source and destination pools differ in layout, layers, dtype or device")
+        self.dst_allocator = dst_allocator
+        self.buffer_bytes_max = int(buffer_bytes_max)
+        self.stager = stager
+        self._buf: Optional[torch.Tensor] = None
+
+    # ------------------------------------------------------------ planning
+
+    def plan(self, src_tables: Sequence[Sequence[int]],
+             dst_pages: Optional[Sequence[int]] = None) -> MigrationPlan:
+        """Allocates and remaps destination pages (see plan_batch)."""
+        return plan_batch(src_tables, self.src.num_pages, self.dst_allocator, dst_pages)
+
+    def upload(self, plan: MigrationPlan):
+        """Both id lists as int32 device tensors, via one pinned copy."""
+        n = plan.n_pages
+        host = torch.empty(2 * n, dtype=torch.int32, pin_memory=True)
+        host[:n] = torch.tensor(plan.src_ids, dtype=torch.int32)
+        host[n:] = torch.tensor(plan.dst_ids, dtype=torch.int32)
+        dev = host.to(self.src.device, non_blocking=True)
+        return dev[:n], dev[n:]
+
+    # ------------------------------------------------------------ movement
+
+    def _buffer(self, layers: int, n: int) -> torch.Tensor:
+        need = (layers, n) + self.src.page_shape
+        numel = layers * n * self.src.page_bytes // torch.empty(0, dtype=self.src.dtype).element_size()
+        if self._buf is None or self._buf.numel() < numel:
+            self._buf = torch.empty(numel, dtype=self.src.dtype, device=self.src.device)
+        return self._buf[:numel].view(need)
+
+    def chunk_layers(self, n: int) -> int:
+        layer_bytes = max(1, n * self.src.page_bytes)
+        return max(1, min(self.src.num_layers, self.buffer_bytes_max // layer_bytes))
+
+    def move_pages(self, src_ids: torch.Tensor, dst_ids: torch.Tensor, mode: str = "buffer",
+                   layers_per_chunk: Optional[int] = None,
+                   host_buf: Optional[torch.Tensor] = None) -> None:
+        n = src_ids.numel()
+        if n == 0:
+            return
+        L = self.src.num_layers
+        if mode == "fused":
+            ops.move(self.src, src_ids, self.dst, dst_ids)
+        elif mode == "buffer":
+            k = layers_per_chunk or self.chunk_layers(n)
+            buf = self._buffer(min(k, L), n)
+            for lb in range(0, L, k):
+                le = min(L, lb + k)
+                ops.pack(self.src, src_ids, buf[: le - lb], layer_begin=lb, layer_end=le)
+                ops.unpack(buf[: le - lb], self.dst, dst_ids, layer_begin=lb, layer_end=le)
+        elif mode == "pinned":
+            from .kv_utils import chunk_layers
+            k = layers_per_chunk or chunk_layers(L, n * self.src.page_bytes)
+            slot = k * n * self.src.page_bytes
+            if self.stager is None or self.stager.slot_bytes < slot:
+                if self.stager is not None:
+                    torch.cuda.current_stream(self.src.device).synchronize()
+                    self.stager.close()
+                self.stager = ops.Stager(-(-slot // 256) * 256, 3, self.src.device)
+            if host_buf is None:
+                host_buf = torch.empty(L * n * self.src.page_bytes, dtype=torch.uint8, pin_memory=True)
+            self.stager.roundtrip(self.src, src_ids, self.dst, dst_ids, host_buf, k)
+        else:
+            raise ValueError(f"unknown mode {mode!r}")
+
+    def promote(self, src_tables: Sequence[Sequence[int]], dst_pages: Optional[Sequence[int]] = None,
+                mode: str = "buffer", layers_per_chunk: Optional[int] = None,
+                host_buf: Optional[torch.Tensor] = None) -> MigrationPlan:
+        """Plans, uploads and moves a batch of requests; returns the plan.  The
+        work is enqueued on the current stream (synchronize to wait)."""
+        plan = self.plan(src_tables, dst_pages)
+        if plan.n_pages:
+            s_ids, d_ids = self.upload(plan)
+            self.move_pages(s_ids, d_ids, mode, layers_per_chunk, host_buf)
+        return plan

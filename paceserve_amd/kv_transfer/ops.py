@@ -1,0 +1,287 @@
+"""Tensor-level KV page movement over libpace_kv (HIP kernels for gfx950).
+
+A *pool* is the per-layer paged KV cache of one instance: a list of L device
+tensors, each contiguous with shape [num_pages, 2, page_size, num_kv_heads,
+head_dim] (the layout of FlashinferAttentionWrapper.gpu_cache,
+paceserve/model_executor/attention/flashinfer_attention_wrapper.py:53-73).
+A *transfer buffer* is one contiguous tensor [L, n, 2, page_size, H, D]: the
+layout KVhelper.get_kv_cache returns (paceserve/kv_transfer/kv_utils.py:44).
+
+Everything here enqueues work on the caller's current HIP stream and returns
+without waiting, like a torch op.  Page ids may be given as a device int32
+tensor (used as is) or as host data (copied to the device on the current
+stream through pinned memory).  Ids outside [0, num_pages) are never
+dereferenced by the kernels; the host-side entry points above this module
+validate ids before they reach the device.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence, Tuple, Union
+
+import torch
+
+from .. import _native
+
+IdsLike = Union[torch.Tensor, Sequence[int]]
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class PagedPool:
+    """Per-layer paged KV tensors of one cache, plus their cached layer table."""
+
+    def __init__(self, layers: Sequence[torch.Tensor]):
+        layers = list(layers)
+        if not layers:
+            raise ValueError("a pool needs at least one layer tensor")
+        first = layers[0]
+        if first.dim() != 5 or first.shape[1] != 2:
+            raise ValueError(
+                f"layer tensors must be [num_pages, 2, page_size, num_kv_heads, head_dim], got {tuple(first.shape)}")
+        for i, t in enumerate(layers):
+            if t.shape != first.shape or t.dtype != first.dtype or t.device != first.device:
+                raise ValueError(f"layer {i} differs in shape/dtype/device from layer 0")
+            if not t.is_contiguous():
+                raise ValueError(f"layer {i} is not contiguous")
+        if first.device.type != "cuda":
+            raise ValueError("pool layers must be device tensors")
+        self.layers: List[torch.Tensor] = layers
+        self.num_layers = len(layers)
+        self.num_pages = int(first.shape[0])
+        self.page_shape: Tuple[int, ...] = tuple(int(s) for s in first.shape[1:])
+        self.dtype = first.dtype
+        self.device = first.device
+        self.page_bytes = int(first[0].numel()) * first.element_size()
+        if self.page_bytes % 16:
+            raise ValueError(f"page bytes ({self.page_bytes}) must be a multiple of 16")
+        self._table = _native.pointer_array([t.data_ptr() for t in layers])
+        self._table_addr = ctypes.addressof(self._table)
+
+    def table(self, layer_begin: int = 0) -> int:
+        """Address of the layer table entry for layer `layer_begin`."""
+        return self._table_addr + layer_begin * ctypes.sizeof(ctypes.c_void_p)
+
+    def holds(self, layers: Sequence[torch.Tensor]) -> bool:
+        """True if `layers` are exactly the tensors this pool was built from."""
+        return len(layers) == self.num_layers and all(a is b for a, b in zip(layers, self.layers))
+
+    def compatible(self, other: "PagedPool") -> bool:
+        return (self.page_shape == other.page_shape and self.dtype == other.dtype
+                and self.device == other.device)
+
+    def layer_range(self, layer_begin: int, layer_end: Optional[int]) -> Tuple[int, int]:
+        end = self.num_layers if layer_end is None else layer_end
+        if not (0 <= layer_begin <= end <= self.num_layers):
+            raise ValueError(f"layer range [{layer_begin}, {end}) outside [0, {self.num_layers})")
+        return layer_begin, end
+
+
+def as_pool(pool_or_layers) -> PagedPool:
+    return pool_or_layers if isinstance(pool_or_layers, PagedPool) else PagedPool(pool_or_layers)
+
+
+def device_ids(ids: IdsLike, device: torch.device) -> torch.Tensor:
+    """Page ids as a contiguous int32 device tensor (host data is copied
+    asynchronously on the current stream through pinned memory)."""
+    if isinstance(ids, torch.Tensor):
+        if ids.device.type == "cuda":
+            if ids.dtype != torch.int32 or not ids.is_contiguous() or ids.dim() != 1:
+                raise ValueError("device page ids must be a contiguous 1-D int32 tensor")
+            if ids.device != device:
+                raise ValueError(f"page ids on {ids.device}, pool on {device}")
+            return ids
+        host = ids.to(torch.int32).contiguous().view(-1)
+    else:
+        host = torch.tensor(list(ids), dtype=torch.int32)
+    if host.numel() == 0:
+        return torch.empty(0, dtype=torch.int32, device=device)
+    return host.pin_memory().to(device, non_blocking=True)
+
+
+def _err_ptr(err: Optional[torch.Tensor]) -> Optional[int]:
+    if err is None:
+        return None
+    if err.dtype != torch.int32 or err.device.type != "cuda" or err.numel() < 1:
+        raise ValueError("err must be an int32 device tensor with at least one element")
+    return err.data_ptr()
+
+
+def _check_buffer(buf: torch.Tensor, pool: PagedPool, n_layers: int, n_pages: int, what: str) -> int:
+    """Validates a transfer buffer [n_layers, >= n_pages, *page_shape]; returns
+    its layer stride in bytes."""
+    if buf.device != pool.device or buf.dtype != pool.dtype:
+        raise ValueError(f"{what}: buffer dtype/device ({buf.dtype}, {buf.device}) "
+                         f"differ from the pool's ({pool.dtype}, {pool.device})")
+    if not buf.is_contiguous() or buf.dim() != 2 + len(pool.page_shape):
+        raise ValueError(f"{what}: buffer must be a contiguous [L, n, *page_shape] tensor")
+    if tuple(buf.shape[2:]) != pool.page_shape:
+        raise ValueError(f"{what}: buffer page shape {tuple(buf.shape[2:])} != pool page shape {pool.page_shape}")
+    if buf.shape[0] < n_layers or buf.shape[1] < n_pages:
+        raise ValueError(f"{what}: buffer {tuple(buf.shape[:2])} holds fewer than "
+                         f"({n_layers}, {n_pages}) layer pages")
+    return buf.stride(0) * buf.element_size()
+
+
+def pack(src, page_ids: IdsLike, out: Optional[torch.Tensor] = None, *,
+         layer_begin: int = 0, layer_end: Optional[int] = None,
+         err: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[l - layer_begin, j] = src.layers[l][page_ids[j]] (whole pages, bit-exact).
+
+    Returns the [layers, n, *page_shape] transfer buffer (`out` if given)."""
+    pool = as_pool(src)
+    lb, le = pool.layer_range(layer_begin, layer_end)
+    ids = device_ids(page_ids, pool.device)
+    n = ids.numel()
+    if out is None:
+        out = torch.empty((le - lb, n) + pool.page_shape, dtype=pool.dtype, device=pool.device)
+    stride = _check_buffer(out, pool, le - lb, n, "pack")
+    _native.check(_native.load().pace_kv_pack(
+        pool.table(lb), le - lb, pool.num_pages, ids.data_ptr() if n else None, n,
+        pool.page_bytes, out.data_ptr(), stride, _err_ptr(err), _stream_handle(pool.device)))
+    return out
+
+
+def unpack(buf: torch.Tensor, dst, page_ids: IdsLike, *, layer_begin: int = 0,
+           layer_end: Optional[int] = None, err: Optional[torch.Tensor] = None) -> None:
+    """dst.layers[l][page_ids[j]] = buf[l - layer_begin, j]; other pages untouched.
+
+    page_ids must not repeat a page (KVhelper removes repeats on the host)."""
+    pool = as_pool(dst)
+    lb, le = pool.layer_range(layer_begin, layer_end)
+    ids = device_ids(page_ids, pool.device)
+    n = ids.numel()
+    stride = _check_buffer(buf, pool, le - lb, n, "unpack")
+    _native.check(_native.load().pace_kv_unpack(
+        buf.data_ptr(), stride, pool.table(lb), le - lb, pool.num_pages,
+        ids.data_ptr() if n else None, n, pool.page_bytes, _err_ptr(err),
+        _stream_handle(pool.device)))
+
+
+def move(src, src_ids: IdsLike, dst, dst_ids: IdsLike, *, layer_begin: int = 0,
+         layer_end: Optional[int] = None, err: Optional[torch.Tensor] = None) -> None:
+    """dst.layers[l][dst_ids[j]] = src.layers[l][src_ids[j]], one fused pass with
+    no transfer buffer (same destination bytes as pack followed by unpack)."""
+    sp, dp = as_pool(src), as_pool(dst)
+    if not sp.compatible(dp) or sp.num_layers != dp.num_layers:
+        raise ValueError("source and destination pools differ in layout, layers, dtype or device")
+    lb, le = sp.layer_range(layer_begin, layer_end)
+    s_ids = device_ids(src_ids, sp.device)
+    d_ids = device_ids(dst_ids, dp.device)
+    if s_ids.numel() != d_ids.numel():
+        raise ValueError(f"{s_ids.numel()} source ids but {d_ids.numel()} destination ids")
+    n = s_ids.numel()
+    if n == 0 or le == lb:
+        return
+    _native.check(_native.load().pace_kv_move(
+        sp.table(lb), sp.num_pages, s_ids.data_ptr(), dp.table(lb), dp.num_pages,
+        d_ids.data_ptr(), le - lb, n, sp.page_bytes, _err_ptr(err), _stream_handle(sp.device)))
+
+
+class Stager:
+    """Pinned-host staging pipeline (pace_kv_stager): device slot rings, a D2H
+    and an H2D side stream, and the events that order them.
+
+    Host tensors handed to a call are kept alive until the caller's stream has
+    passed the point where the call's copies finish.  One host thread at a
+    time may drive a stager."""
+
+    def __init__(self, slot_bytes: int, num_slots: int = 3, device: Optional[torch.device] = None):
+        self.device = torch.device(device) if device is not None else torch.device(
+            "cuda", torch.cuda.current_device())
+        handle = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            _native.check(_native.load().pace_kv_stager_create(int(slot_bytes), int(num_slots),
+                                                               ctypes.byref(handle)))
+        self._handle = handle.value
+        self.slot_bytes = int(slot_bytes)
+        self.num_slots = int(num_slots)
+        self._inflight: list = []
+
+    def _keep(self, *objs) -> None:
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        self._inflight = [(e, o) for e, o in self._inflight if not e.query()]
+        self._inflight.append((ev, objs))
+
+    def _require(self):
+        if self._handle is None:
+            raise RuntimeError("stager is closed")
+        return self._handle
+
+    @staticmethod
+    def _host(t: torch.Tensor, pool: PagedPool, n_layers: int, n: int, what: str) -> None:
+        if t.device.type != "cpu" or not t.is_contiguous() or t.dtype != pool.dtype:
+            raise ValueError(f"{what}: host buffer must be a contiguous CPU tensor of {pool.dtype}")
+        need = n_layers * n * pool.page_bytes
+        if t.numel() * t.element_size() < need:
+            raise ValueError(f"{what}: host buffer holds {t.numel() * t.element_size()} bytes, needs {need}")
+
+    def pack_to_host(self, src, page_ids: IdsLike, host_out: torch.Tensor, layers_per_chunk: int,
+                     *, layer_begin: int = 0, layer_end: Optional[int] = None,
+                     err: Optional[torch.Tensor] = None) -> torch.Tensor:
+        pool = as_pool(src)
+        lb, le = pool.layer_range(layer_begin, layer_end)
+        ids = device_ids(page_ids, pool.device)
+        n = ids.numel()
+        self._host(host_out, pool, le - lb, n, "pack_to_host")
+        _native.check(_native.load().pace_kv_pack_to_host(
+            self._require(), pool.table(lb), le - lb, pool.num_pages, ids.data_ptr() if n else None,
+            n, pool.page_bytes, int(layers_per_chunk), host_out.data_ptr(), _err_ptr(err),
+            _stream_handle(pool.device)))
+        self._keep(host_out, ids)
+        return host_out
+
+    def unpack_from_host(self, host_in: torch.Tensor, dst, page_ids: IdsLike, layers_per_chunk: int,
+                         *, layer_begin: int = 0, layer_end: Optional[int] = None,
+                         err: Optional[torch.Tensor] = None) -> None:
+        pool = as_pool(dst)
+        lb, le = pool.layer_range(layer_begin, layer_end)
+        ids = device_ids(page_ids, pool.device)
+        n = ids.numel()
+        self._host(host_in, pool, le - lb, n, "unpack_from_host")
+        _native.check(_native.load().pace_kv_unpack_from_host(
+            self._require(), host_in.data_ptr(), pool.table(lb), le - lb, pool.num_pages,
+            ids.data_ptr() if n else None, n, pool.page_bytes, int(layers_per_chunk), _err_ptr(err),
+            _stream_handle(pool.device)))
+        self._keep(host_in, ids)
+
+    def roundtrip(self, src, src_ids: IdsLike, dst, dst_ids: IdsLike, host_buf: torch.Tensor,
+                  layers_per_chunk: int, *, err: Optional[torch.Tensor] = None) -> None:
+        sp, dp = as_pool(src), as_pool(dst)
+        if not sp.compatible(dp) or sp.num_layers != dp.num_layers:
+            raise ValueError("source and destination pools differ in layout, layers, dtype or device")
+        s_ids = device_ids(src_ids, sp.device)
+        d_ids = device_ids(dst_ids, dp.device)
+        if s_ids.numel() != d_ids.numel():
+            raise ValueError(f"{s_ids.numel()} source ids but {d_ids.numel()} destination ids")
+        n = s_ids.numel()
+        if host_buf.device.type != "cpu" or not host_buf.is_contiguous():
+            raise ValueError("roundtrip: host buffer must be a contiguous CPU tensor")
+        _native.check(_native.load().pace_kv_roundtrip(
+            self._require(), sp.table(), sp.num_pages, s_ids.data_ptr() if n else None, dp.table(),
+            dp.num_pages, d_ids.data_ptr() if n else None, sp.num_layers, n, sp.page_bytes,
+            int(layers_per_chunk), host_buf.data_ptr(), host_buf.numel() * host_buf.element_size(),
+            _err_ptr(err), _stream_handle(sp.device)))
+        self._keep(host_buf, s_ids, d_ids)
+
+    def close(self) -> None:
+        if self._handle is not None:
+            handle, self._handle = self._handle, None
+            with torch.cuda.device(self.device):
+                _native.check(_native.load().pace_kv_stager_destroy(handle))
+            self._inflight.clear()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,97 @@
+"""Worker-side migration methods: the caller boundary of the path.
+
+Mirrors the three RPC methods of BaseWorker that reach KVhelper
+(paceserve/worker/base_worker.py:235-281) with the same return shapes:
+  - _get_kv_cache(seq)        -> (kv_cache, kv_indices, local_rank), then frees
+                                 the sequence's source pages (:236-240);
+  - _get_kv_cache_nofree(seq) -> same without the free (preemption swap-out,
+                                 :245-247);
+  - _insert_kv_cache(seq, kv_obj, device) -> KVStatus, or False when the
+    destination cannot hold the sequence (:249-281).
+
+Two reference defects are not reproduced: the allocate time is reported as
+a positive duration (the reference subtracts the later stamp from the earlier
+one, :280), and when the last logical block has P-1 empty slots the
+reference inserts the same pages twice (:265-277); one insert leaves the same
+bytes.
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass
+from typing import Dict
+
+from ..core.block_manager import BlockSpaceManager
+
+
+@dataclass
+class KVStatus:
+    status: bool
+    insertion_time: float
+    allocate_time: float
+
+
+class WorkerSequenceManager:
+    """The worker's sequence map plus its clone of the block manager
+    (paceserve/core/sequence_manager/worker_sequence_manager.py:13-66)."""
+
+    def __init__(self, block_size: int, num_gpu_blocks: int, max_model_len=None, free_list=None):
+        self.seq_map: Dict[str, object] = {}
+        self.block_manager = BlockSpaceManager(block_size, num_gpu_blocks, max_model_len,
+                                               free_list=free_list)
+
+    def add_seq(self, seq) -> None:
+        self.seq_map[seq.seq_id] = seq
+
+    def _free_seq(self, seq_id: str) -> None:
+        if seq_id not in self.seq_map:
+            raise KeyError(seq_id)
+        seq = self.seq_map[seq_id]
+        if self.block_manager.is_allocated(seq):
+            self.block_manager.free(seq)
+        del self.seq_map[seq_id]
+
+    def _get_block_table(self, seq):
+        return self.block_manager.get_block_table(seq)
+
+
+class KVWorkerMixin:
+    """Provides the worker's KV methods; the host class supplies
+    `kvhelper` (a KVhelper), `seq_manager` and `local_rank`."""
+
+    def _get_kv_cache(self, seq):
+        kv_cache, kv_indices = self.kvhelper.get_kv_cache(seq, self.seq_manager)
+        self.seq_manager._free_seq(seq.seq_id)
+        return (kv_cache, kv_indices, self.local_rank)
+
+    def _get_kv_cache_nofree(self, seq):
+        kv_cache, kv_indices = self.kvhelper.get_kv_cache(seq, self.seq_manager)
+        return (kv_cache, kv_indices, self.local_rank)
+
+    def _insert_kv_cache(self, seq, kv_obj, device):
+        block_len = len(kv_obj.kv_indices)
+        cached_content = kv_obj.kv_cache
+        allocate_start = time.monotonic()
+        bm = self.seq_manager.block_manager
+        if bm.get_num_free_gpu_blocks() >= bm.get_num_initial_blocks(seq):
+            self.seq_manager.add_seq(seq)
+            bm.allocate(seq)
+        else:
+            return False
+        kv_indices = self.seq_manager._get_block_table(seq)
+        insert_start = time.monotonic()
+        # A destination table one page longer than the source (the first
+        # generated token opened a page) leaves that last page untouched.
+        ids = kv_indices if len(kv_indices) == block_len else kv_indices[:-1]
+        status = self.kvhelper.insert_kv_cache(cached_content, ids, device)
+        insert_time = time.monotonic() - insert_start
+        return KVStatus(status, insert_time, insert_start - allocate_start)
+
+
+class KVWorker(KVWorkerMixin):
+    """A standalone worker holding one KVhelper and its sequence manager."""
+
+    def __init__(self, kvhelper, seq_manager: WorkerSequenceManager, local_rank: int = 0):
+        self.kvhelper = kvhelper
+        self.seq_manager = seq_manager
+        self.local_rank = local_rank

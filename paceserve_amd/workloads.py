@@ -1,0 +1,199 @@
+"""Seeded synthetic migration workloads at the reference's KV shapes.
+
+Each workload fixes the cache shape, the source/destination pool sizes, the
+request lengths and how the source pool's free list is fragmented, so that the
+benchmark and the tests build identical source block tables and pages:
+
+  config 1  Llama-3-8B KV (32 layers, 8 KV heads, head_dim 128, page 16), fp16:
+            one 512-token request (32 pages) at seeded random pages of a
+            2048-page pool, values N(0,1).
+  config 2  same shape, bf16: 16 requests, lengths lognormal(median 1024,
+            sigma 1.0) clipped to [128, 8192]; 16384-page pools; the source
+            free list is a seeded permutation; separate fresh destination pool.
+  config 3  Llama-2-7B KV (32 KV heads), fp16: 8 requests of 4095 tokens
+            (256 pages each, last page 15/16 full); 4096-page pools, permuted;
+            migrated through pinned host memory, one layer per chunk.
+  config 4  Llama-3-8B KV, bf16, values uniform[-4, 4]: one 32768-token
+            request filling a 2048-page pool in permuted order; on-device and
+            pinned-host variants.
+  config 5  Llama-3-70B KV (80 layers, 8 KV heads), bf16: 256 requests of
+            U{64..2048} tokens; 20480-page pools; a seeded permutation of the
+            source pool dealt to requests round-robin one page at a time;
+            moved in 8-layer chunks.
+  promote4k Llama-3-8B KV, bf16: one 4096-token request (256 pages) in a
+            2048-page pool (the promote-latency workload).
+
+Seed 1000 + c for config c (1100 for promote4k).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import numpy as np
+import torch
+
+
+@dataclass(frozen=True)
+class KVShape:
+    num_layers: int
+    num_kv_heads: int
+    head_dim: int
+    page_size: int
+    dtype: torch.dtype
+
+    @property
+    def page_shape(self):
+        return (2, self.page_size, self.num_kv_heads, self.head_dim)
+
+    @property
+    def page_bytes(self) -> int:
+        return 2 * self.page_size * self.num_kv_heads * self.head_dim * torch.empty(0, dtype=self.dtype).element_size()
+
+
+@dataclass
+class Workload:
+    name: str
+    description: str
+    shape: KVShape
+    src_pool_pages: int
+    dst_pool_pages: int
+    lengths: List[int]
+    src_tables: List[List[int]]
+    seed: int
+    init: str = "normal"             # "normal" = N(0,1), "uniform4" = U[-4, 4]
+    staging: str = "device"          # "device", "pinned" or "both"
+    layers_per_chunk: Optional[int] = None
+    dst_free: Optional[List[int]] = None
+    notes: dict = field(default_factory=dict)
+
+    @property
+    def n_pages(self) -> int:
+        return sum(len(t) for t in self.src_tables)
+
+    @property
+    def payload_bytes(self) -> int:
+        return self.shape.num_layers * self.n_pages * self.shape.page_bytes
+
+    def summary(self) -> dict:
+        return {
+            "workload": self.name,
+            "description": self.description,
+            "layers": self.shape.num_layers,
+            "kv_heads": self.shape.num_kv_heads,
+            "head_dim": self.shape.head_dim,
+            "page_size": self.shape.page_size,
+            "cache_dtype": str(self.shape.dtype).replace("torch.", ""),
+            "requests": len(self.src_tables),
+            "pages": self.n_pages,
+            "src_pool_pages": self.src_pool_pages,
+            "dst_pool_pages": self.dst_pool_pages,
+            "payload_bytes": self.payload_bytes,
+            "seed": self.seed,
+        }
+
+
+LLAMA3_8B = dict(num_layers=32, num_kv_heads=8, head_dim=128, page_size=16)
+
+
+def _pages(tokens: int, page_size: int) -> int:
+    return -(-tokens // page_size)
+
+
+def _lifo_tables(free_list: List[int], lengths: List[int], page_size: int) -> List[List[int]]:
+    """Requests allocate in order, each popping its pages from the end of the
+    free list (the reference allocator's order)."""
+    free = list(free_list)
+    tables = []
+    for n_tok in lengths:
+        n = _pages(n_tok, page_size)
+        if n > len(free):
+            raise ValueError("pool too small for the workload")
+        got = free[-n:]
+        del free[-n:]
+        got.reverse()
+        tables.append(got)
+    return tables
+
+
+def config(c) -> Workload:
+    if c == 1:
+        seed = 1001
+        rng = np.random.default_rng(seed)
+        shape = KVShape(**LLAMA3_8B, dtype=torch.float16)
+        lengths = [512]
+        tables = [rng.permutation(2048)[:32].tolist()]
+        return Workload("config1", "1 x 512-token request, Llama-3-8B KV, fp16, 2048-page pool",
+                        shape, 2048, 2048, lengths, tables, seed)
+    if c == 2:
+        seed = 1002
+        rng = np.random.default_rng(seed)
+        shape = KVShape(**LLAMA3_8B, dtype=torch.bfloat16)
+        raw = rng.lognormal(mean=np.log(1024.0), sigma=1.0, size=16)
+        lengths = np.clip(np.rint(raw), 128, 8192).astype(int).tolist()
+        free = rng.permutation(16384).tolist()
+        tables = _lifo_tables(free, lengths, 16)
+        return Workload("config2", "16 requests, lognormal(median 1024, sigma 1.0) tokens clipped "
+                        "[128, 8192], Llama-3-8B KV, bf16, 16384-page pools, fragmented source free list",
+                        shape, 16384, 16384, lengths, tables, seed)
+    if c == 3:
+        seed = 1003
+        rng = np.random.default_rng(seed)
+        shape = KVShape(num_layers=32, num_kv_heads=32, head_dim=128, page_size=16, dtype=torch.float16)
+        lengths = [4095] * 8
+        free = rng.permutation(4096).tolist()
+        tables = _lifo_tables(free, lengths, 16)
+        return Workload("config3", "8 x 4095-token requests (partial last page), Llama-2-7B KV, fp16, "
+                        "4096-page pools, pinned-host round trip per layer",
+                        shape, 4096, 4096, lengths, tables, seed, staging="pinned", layers_per_chunk=1)
+    if c == 4:
+        seed = 1004
+        rng = np.random.default_rng(seed)
+        shape = KVShape(**LLAMA3_8B, dtype=torch.bfloat16)
+        lengths = [32768]
+        tables = [rng.permutation(2048).tolist()]
+        return Workload("config4", "1 x 32768-token request, Llama-3-8B KV, bf16, values U[-4,4], "
+                        "2048-page pool in permuted order, on-device and pinned-host",
+                        shape, 2048, 2048, lengths, tables, seed, init="uniform4", staging="both")
+    if c == 5:
+        seed = 1005
+        rng = np.random.default_rng(seed)
+        shape = KVShape(num_layers=80, num_kv_heads=8, head_dim=128, page_size=16, dtype=torch.bfloat16)
+        lengths = rng.integers(64, 2049, size=256).tolist()
+        need = [_pages(n, 16) for n in lengths]
+        perm = rng.permutation(20480).tolist()
+        tables: List[List[int]] = [[] for _ in lengths]
+        k = 0
+        while any(len(t) < n for t, n in zip(tables, need)):
+            for r in range(len(lengths)):
+                if len(tables[r]) < need[r]:
+                    tables[r].append(perm[k])
+                    k += 1
+        return Workload("config5", "256 requests U{64..2048} tokens, Llama-3-70B KV (80 layers), bf16, "
+                        "20480-page pools dealt round-robin (heavily fragmented), 8-layer chunks",
+                        shape, 20480, 20480, lengths, tables, seed, layers_per_chunk=8)
+    if c == "promote4k":
+        seed = 1100
+        rng = np.random.default_rng(seed)
+        shape = KVShape(**LLAMA3_8B, dtype=torch.bfloat16)
+        lengths = [4096]
+        tables = [rng.permutation(2048)[:256].tolist()]
+        return Workload("promote4k", "1 x 4096-token request, Llama-3-8B KV, bf16, 2048-page pools",
+                        shape, 2048, 2048, lengths, tables, seed)
+    raise ValueError(f"unknown workload {c!r}")
+
+
+def fill_pool(layers_pages: int, shape: KVShape, seed: int, init: str, device) -> List[torch.Tensor]:
+    """Per-layer pool tensors with seeded values (generated on `device`)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    out = []
+    for _ in range(shape.num_layers):
+        t = torch.empty((layers_pages,) + shape.page_shape, dtype=shape.dtype, device=device)
+        if init == "normal":
+            t.normal_(generator=g)
+        elif init == "uniform4":
+            t.uniform_(-4.0, 4.0, generator=g)
+        else:
+            raise ValueError(init)
+        out.append(t)
+    return out

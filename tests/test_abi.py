@@ -1,0 +1,94 @@
+"""The C-ABI library: loads, exports every symbol include/pace_kv.h declares,
+and rejects bad arguments on the host before any device work (no GPU here)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from paceserve_amd import _native
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "pace_kv.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(pace_kv_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _native.LIB_PATH.exists():
+        pytest.fail(f"{_native.LIB_PATH} is not built (run python -m paceserve_amd.build)")
+    return _native.load()
+
+
+def test_header_declares_the_bound_functions():
+    assert declared_functions() == sorted(_native.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    assert lib.pace_kv_abi_version() == _native.ABI_VERSION
+    text = HEADER.read_text()
+    assert f"#define PACE_KV_ABI_VERSION {_native.ABI_VERSION}" in text
+    assert f"#define PACE_KV_MAX_LAYERS_PER_LAUNCH {_native.MAX_LAYERS_PER_LAUNCH}" in text
+
+
+def _layers(n, base=0x10000):
+    return _native.pointer_array([base + i * 0x100000 for i in range(n)])
+
+
+def test_empty_work_is_a_no_op(lib):
+    # zero layers or zero pages: success without touching the device
+    assert lib.pace_kv_pack(None, 0, 10, None, 5, 65536, None, 0, None, None) == 0
+    assert lib.pace_kv_pack(_layers(2), 2, 10, None, 0, 65536, None, 0, None, None) == 0
+    assert lib.pace_kv_unpack(None, 0, _layers(2), 2, 10, None, 0, 65536, None, None) == 0
+    assert lib.pace_kv_move(None, 10, None, None, 10, None, 0, 3, 65536, None, None) == 0
+
+
+@pytest.mark.parametrize("call,code,msg", [
+    (lambda L: L.pace_kv_pack(_layers(2), -1, 10, 0x100, 4, 65536, 0x1000, 4 * 65536, None, None),
+     _native.PACE_KV_EINVAL, "num_layers"),
+    (lambda L: L.pace_kv_pack(_layers(2), 2, 10, None, 4, 65536, 0x1000, 4 * 65536, None, None),
+     _native.PACE_KV_EINVAL, "NULL"),
+    (lambda L: L.pace_kv_pack(_layers(2), 2, 10, 0x100, 4, 65536, 0x1000, 65536, None, None),
+     _native.PACE_KV_ERANGE, "out_layer_stride"),
+    (lambda L: L.pace_kv_pack(_layers(2), 2, 10, 0x100, 4, 65536, 0x1000, 4 * 65536 + 8, None, None),
+     _native.PACE_KV_EINVAL, "stride not a multiple of 16"),
+    (lambda L: L.pace_kv_pack(_layers(2), 2, 10, 0x100, 4, 65530, 0x1000, 4 * 65536, None, None),
+     _native.PACE_KV_EINVAL, "page_bytes must be a positive multiple of 16"),
+    (lambda L: L.pace_kv_pack(_layers(2), 2, 10, 0x100, 4, 100, 0x1000, 4 * 112, None, None),
+     _native.PACE_KV_EINVAL, "page_bytes"),
+    (lambda L: L.pace_kv_pack(_native.pointer_array([0x10000, 0x10008]), 2, 10, 0x100, 4, 65536,
+                              0x1000, 4 * 65536, None, None),
+     _native.PACE_KV_EINVAL, "16-byte aligned"),
+    (lambda L: L.pace_kv_pack(_native.pointer_array([0x10000, 0]), 2, 10, 0x100, 4, 65536,
+                              0x1000, 4 * 65536, None, None),
+     _native.PACE_KV_EINVAL, "NULL"),
+    (lambda L: L.pace_kv_unpack(0x1000, 65536, _layers(2), 2, 10, 0x100, 4, 65536, None, None),
+     _native.PACE_KV_ERANGE, "buf_layer_stride"),
+    (lambda L: L.pace_kv_move(_layers(2), 10, 0x100, _layers(2), 10, None, 2, 4, 65536, None, None),
+     _native.PACE_KV_EINVAL, "NULL page ids"),
+    (lambda L: L.pace_kv_move(_layers(2), 10, 0x102, _layers(2), 10, 0x100, 2, 4, 65536, None, None),
+     _native.PACE_KV_EINVAL, "4-byte aligned"),
+    (lambda L: L.pace_kv_stager_create(1000, 3, ctypes.byref(ctypes.c_void_p())),
+     _native.PACE_KV_EINVAL, "slot_bytes"),
+    (lambda L: L.pace_kv_stager_create(1 << 20, 1, ctypes.byref(ctypes.c_void_p())),
+     _native.PACE_KV_EINVAL, "num_slots"),
+    (lambda L: L.pace_kv_pack_to_host(None, _layers(1), 1, 10, 0x100, 1, 65536, 1, 0x1000, None, None),
+     _native.PACE_KV_EINVAL, "stager is NULL"),
+])
+def test_argument_errors_are_reported_on_the_host(lib, call, code, msg):
+    assert call(lib) == code
+    assert msg in lib.pace_kv_last_error().decode()
+
+
+def test_check_raises_with_message(lib):
+    rc = lib.pace_kv_pack(_layers(2), -1, 10, 0x100, 4, 65536, 0x1000, 4 * 65536, None, None)
+    with pytest.raises(_native.PaceKVError, match="num_layers"):
+        _native.check(rc)

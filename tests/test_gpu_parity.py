@@ -1,0 +1,227 @@
+"""Parity of the HIP path (libpace_kv.so through its C ABI) with the oracle,
+the golden fixtures and torch's own device gather/scatter.  Bit-exact: the
+path copies bytes, so every comparison is on raw integer words."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as orc
+from paceserve_amd import _native
+from paceserve_amd.kv_transfer import ops
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+WORD = {torch.float16: torch.int16, torch.bfloat16: torch.int16, torch.float32: torch.int32,
+        torch.float8_e4m3fn: torch.uint8, torch.uint8: torch.uint8}
+
+
+def words(t):
+    return t.view(WORD[t.dtype])
+
+
+def same(a, b):
+    return a.shape == b.shape and torch.equal(words(a), words(b))
+
+
+def load(name):
+    with np.load(GOLDEN / f"case_{name}.npz", allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def to_dev(arr, kind, gpu):
+    dt = torch.float16 if kind == "fp16" else torch.bfloat16
+    return torch.from_numpy(arr.astype(np.int16)).to(gpu).view(dt)
+
+
+def rand_pool(L, pages, shape, dtype, gpu, seed):
+    g = torch.Generator(device=gpu).manual_seed(seed)
+    if dtype in (torch.float16, torch.bfloat16, torch.float32):
+        return [torch.randn((pages,) + shape, generator=g, device=gpu, dtype=torch.float32).to(dtype)
+                for _ in range(L)]
+    return [torch.randint(0, 256, (pages,) + shape, generator=g, device=gpu, dtype=torch.uint8).view(dtype)
+            for _ in range(L)]
+
+
+@pytest.mark.parametrize("name", ["fp16_partial", "bf16_nplus1", "fp16_batch2"])
+def test_golden_cases(gpu, name):
+    c = load(name)
+    kind = str(c["kind"])
+    src = [to_dev(s, kind, gpu) for s in c["src"]]
+    dst = [to_dev(d, kind, gpu) for d in c["dst_before"]]
+    buf = ops.pack(src, c["src_table"].tolist())
+    torch.cuda.synchronize()
+    assert np.array_equal(words(buf).cpu().numpy().astype(np.uint16), c["packed"])
+    ops.unpack(buf, dst, c["dst_ids"].tolist())
+    torch.cuda.synchronize()
+    got = np.stack([words(d).cpu().numpy().astype(np.uint16) for d in dst])
+    assert np.array_equal(got, c["dst_after"])
+    # fused move leaves the same destination bytes
+    dst2 = [to_dev(d, kind, gpu) for d in c["dst_before"]]
+    ops.move(src, c["src_table"].tolist(), dst2, c["dst_ids"].tolist())
+    torch.cuda.synchronize()
+    got2 = np.stack([words(d).cpu().numpy().astype(np.uint16) for d in dst2])
+    assert np.array_equal(got2, c["dst_after"])
+
+
+def test_zero_fallback_insert(gpu):
+    c = load("zero_fallback")
+    dst = [to_dev(d, "fp16", gpu) for d in c["dst_before"]]
+    ops.unpack(to_dev(c["packed"], "fp16", gpu), dst, c["dst_ids"].tolist())
+    torch.cuda.synchronize()
+    got = np.stack([words(d).cpu().numpy().astype(np.uint16) for d in dst])
+    assert np.array_equal(got, c["dst_after"])
+
+
+SHAPES = [
+    # (L, pool pages, page shape [2, P, H, D], dtype, n)
+    (1, 8, (2, 16, 8, 128), torch.float16, 3),
+    (3, 40, (2, 16, 8, 128), torch.bfloat16, 17),
+    (32, 64, (2, 16, 8, 128), torch.float16, 32),
+    (2, 16, (2, 16, 32, 128), torch.float16, 9),     # Llama-2-7B page (256 KiB)
+    (4, 33, (2, 16, 1, 128), torch.bfloat16, 20),    # TP=8 slice: 8 KiB page
+    (3, 12, (2, 16, 4, 64), torch.float32, 7),       # 32 KiB page, fp32
+    (2, 20, (2, 16, 8, 128), torch.float8_e4m3fn, 11),  # fp8 page (32 KiB)
+    (2, 9, (2, 4, 2, 8), torch.float16, 5),          # 256 B page: guarded kernel
+    (2, 9, (2, 3, 1, 8), torch.bfloat16, 6),         # 96 B page: guarded kernel
+    (80, 10, (2, 16, 1, 64), torch.bfloat16, 6),     # > 64 layers: two launches
+]
+
+
+@pytest.mark.parametrize("L,pages,shape,dtype,n", SHAPES)
+def test_pack_unpack_move_match_torch_and_oracle(gpu, L, pages, shape, dtype, n):
+    src = rand_pool(L, pages, shape, dtype, gpu, seed=L * 1000 + pages)
+    dst = rand_pool(L, pages, shape, dtype, gpu, seed=L * 1000 + pages + 1)
+    g = torch.Generator().manual_seed(pages)
+    s_ids = torch.randperm(pages, generator=g)[:n]
+    d_ids = torch.randperm(pages, generator=g)[:n]
+    s_dev, d_dev = s_ids.to(gpu), d_ids.to(gpu)
+    ref_buf = torch.stack([torch.index_select(words(s), 0, s_dev) for s in src])
+    ref_dst = [words(d).clone().index_copy_(0, d_dev, ref_buf[i]) for i, d in enumerate(dst)]
+    src_before = [words(s).clone() for s in src]
+
+    buf = ops.pack(src, s_ids.tolist())
+    torch.cuda.synchronize()
+    assert torch.equal(words(buf), ref_buf)
+    dst_a = [d.clone() for d in dst]
+    ops.unpack(buf, dst_a, d_ids.int().to(gpu))
+    dst_b = [d.clone() for d in dst]
+    ops.move(src, s_ids.tolist(), dst_b, d_ids.tolist())
+    torch.cuda.synchronize()
+    for l in range(L):
+        assert torch.equal(words(dst_a[l]), ref_dst[l]), f"unpack layer {l}"
+        assert torch.equal(words(dst_b[l]), ref_dst[l]), f"move layer {l}"
+        assert torch.equal(words(src[l]), src_before[l]), f"source layer {l} written"
+    if L * pages * np.prod(shape) <= 1 << 22:     # oracle on the CPU for small cases
+        np_src = [words(s).cpu().numpy() for s in src]
+        np.testing.assert_array_equal(words(buf).cpu().numpy(), orc.pack(np_src, s_ids.tolist()))
+
+
+def test_layer_ranges_and_preallocated_buffer(gpu):
+    L, pages, shape = 6, 30, (2, 16, 8, 128)
+    src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 1)
+    ids = [29, 0, 13, 7]
+    big = torch.full((3, 10) + shape, 7.0, dtype=torch.bfloat16, device=gpu)   # room for 10 pages
+    ops.pack(src, ids, big, layer_begin=2, layer_end=5)
+    torch.cuda.synchronize()
+    for i, l in enumerate(range(2, 5)):
+        assert same(big[i, :4], src[l][torch.tensor(ids, device=gpu)])
+        assert (big[i, 4:] == 7.0).all()
+
+
+def test_out_of_range_ids_are_skipped_and_counted(gpu):
+    L, pages, shape = 3, 8, (2, 16, 8, 128)
+    src = rand_pool(L, pages, shape, torch.float16, gpu, 2)
+    ids = torch.tensor([1, 8, -1, 5], dtype=torch.int32, device=gpu)   # 8 and -1 are invalid
+    out = torch.full((L, 4) + shape, 3.0, dtype=torch.float16, device=gpu)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ops.pack(src, ids, out, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 2 * L
+    for l in range(L):
+        assert same(out[l, 0], src[l][1]) and same(out[l, 3], src[l][5])
+        assert (out[l, 1] == 3.0).all() and (out[l, 2] == 3.0).all()
+    dst = rand_pool(L, pages, shape, torch.float16, gpu, 3)
+    before = [d.clone() for d in dst]
+    err.zero_()
+    ops.unpack(out, dst, torch.tensor([2, 100, 4, -7], dtype=torch.int32, device=gpu), err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 2 * L
+    for l in range(L):
+        assert same(dst[l][2], out[l, 0]) and same(dst[l][4], out[l, 2])
+        keep = [0, 1, 3, 5, 6, 7]
+        assert same(dst[l][keep], before[l][keep])
+
+
+def test_empty_batch_is_a_no_op(gpu):
+    src = rand_pool(2, 4, (2, 16, 8, 128), torch.float16, gpu, 4)
+    buf = ops.pack(src, [])
+    assert buf.shape == (2, 0, 2, 16, 8, 128)
+    ops.unpack(buf, src, [])
+    ops.move(src, [], src, [])
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("n,layers_per_chunk", [(5, 1), (12, 3), (12, 8), (1, 2)])
+def test_staging_pack_to_host_and_back(gpu, n, layers_per_chunk):
+    L, pages, shape = 7, 16, (2, 16, 8, 128)
+    src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 10 + n)
+    dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 20 + n)
+    g = torch.Generator().manual_seed(n)
+    s_ids = torch.randperm(pages, generator=g)[:n].tolist()
+    d_ids = torch.randperm(pages, generator=g)[:n].tolist()
+    page_bytes = int(np.prod(shape)) * 2
+    with ops.Stager(layers_per_chunk * n * page_bytes, 2) as st:
+        host = torch.empty((L, n) + shape, dtype=torch.bfloat16, pin_memory=True)
+        st.pack_to_host(src, s_ids, host, layers_per_chunk)
+        torch.cuda.current_stream().synchronize()
+        ref = torch.stack([s[torch.tensor(s_ids, device=gpu)] for s in src]).cpu()
+        assert same(host, ref)
+        expect = [words(d).clone() for d in dst]
+        for l in range(L):
+            expect[l][torch.tensor(d_ids, device=gpu)] = words(ref[l]).to(gpu)
+        st.unpack_from_host(host, dst, d_ids, layers_per_chunk)
+        torch.cuda.current_stream().synchronize()
+        for l in range(L):
+            assert torch.equal(words(dst[l]), expect[l]), f"layer {l}"
+        # pageable host memory goes through the same pipeline
+        pageable = ref.clone()
+        dst2 = rand_pool(L, pages, shape, torch.bfloat16, gpu, 20 + n)
+        st.unpack_from_host(pageable, dst2, d_ids, layers_per_chunk)
+        torch.cuda.current_stream().synchronize()
+        for l in range(L):
+            assert torch.equal(words(dst2[l]), expect[l]), f"pageable layer {l}"
+
+
+@pytest.mark.parametrize("slots,host_chunks,layers_per_chunk", [(2, None, 1), (3, 1, 2), (2, 2, 3), (4, None, 5)])
+def test_roundtrip_matches_move(gpu, slots, host_chunks, layers_per_chunk):
+    L, pages, shape, n = 9, 24, (2, 16, 8, 128), 10
+    src = rand_pool(L, pages, shape, torch.float16, gpu, 30)
+    dst = rand_pool(L, pages, shape, torch.float16, gpu, 31)
+    ref = [d.clone() for d in dst]
+    g = torch.Generator().manual_seed(5)
+    s_ids = torch.randperm(pages, generator=g)[:n].tolist()
+    d_ids = torch.randperm(pages, generator=g)[:n].tolist()
+    ops.move(src, s_ids, ref, d_ids)
+    page_bytes = int(np.prod(shape)) * 2
+    chunk = layers_per_chunk * n * page_bytes
+    host_bytes = L * n * page_bytes if host_chunks is None else host_chunks * chunk
+    host = torch.empty(host_bytes, dtype=torch.uint8, pin_memory=True)
+    with ops.Stager(chunk, slots) as st:
+        for rep in range(2):              # back-to-back calls reuse slots and events
+            out = [d.clone() for d in dst]
+            st.roundtrip(src, s_ids, out, d_ids, host, layers_per_chunk)
+            torch.cuda.current_stream().synchronize()
+            for l in range(L):
+                assert same(out[l], ref[l]), f"rep {rep} layer {l}"
+
+
+def test_stager_rejects_oversized_chunks(gpu):
+    src = rand_pool(2, 8, (2, 16, 8, 128), torch.float16, gpu, 40)
+    host = torch.empty((2, 4, 2, 16, 8, 128), dtype=torch.float16, pin_memory=True)
+    with ops.Stager(65536 * 3, 2) as st:         # one layer of 4 pages needs 4 * 65536
+        with pytest.raises(_native.PaceKVError, match="slot holds"):
+            st.pack_to_host(src, [0, 1, 2, 3], host, 1)

@@ -1,0 +1,183 @@
+"""Host-side logic of the path (no GPU): allocator, sequences, planning,
+worker boundary and KVhelper conventions, checked against the oracle."""
+import numpy as np
+import pytest
+
+from oracle import kv_oracle as orc
+from paceserve_amd.core.block_manager import BlockAllocator, BlockSpaceManager, remap_dst_table
+from paceserve_amd.core.kv_cache_obj import KVobj
+from paceserve_amd.core.sequence import Sequence
+from paceserve_amd.kv_transfer.kv_utils import chunk_layers, dedup_keep_last, normalize_page_ids
+from paceserve_amd.kv_transfer.migrate import plan_batch
+from paceserve_amd.kv_transfer.worker import KVStatus, KVWorker, WorkerSequenceManager
+
+
+def test_allocator_matches_oracle_sequence_of_operations():
+    rng = np.random.default_rng(0)
+    free = rng.permutation(64).tolist()
+    prod = BlockAllocator(16, 64, free)
+    ref = orc.BlockAllocator(64, free)
+    for step in range(200):
+        if rng.random() < 0.6 and ref.num_free():
+            n = int(rng.integers(0, ref.num_free() + 1))
+            assert prod.allocate_many(n) == orc.allocate_table(ref, n)
+        else:
+            k = int(rng.integers(0, 5))
+            pages = rng.integers(0, 64, k).tolist()
+            prod.free_many(pages)
+            for p in pages:
+                ref.free(p)
+        assert prod.free_blocks == ref.free_blocks
+
+
+def test_allocate_many_is_all_or_nothing():
+    a = BlockAllocator(16, 3)
+    with pytest.raises(ValueError, match="Out of memory"):
+        a.allocate_many(4)
+    assert a.get_num_free_blocks() == 3
+    assert a.allocate_many(3) == [2, 1, 0]
+
+
+def test_sequence_logical_blocks():
+    for n in [1, 15, 16, 17, 4095, 4096]:
+        s = Sequence.of_length("s", n, 16)
+        assert len(s.logical_token_blocks) == orc.pages_for_tokens(n, 16)
+        assert s.logical_token_blocks[-1].num_tokens == orc.last_page_len(n, 16)
+    s = Sequence.of_length("s", 16, 16)
+    s.append_token_id(7)                    # first generated token opens page 2
+    assert len(s.logical_token_blocks) == 2
+    assert s.logical_token_blocks[-1].get_num_empty_slots() == 15
+
+
+def test_block_space_manager_allocate_free():
+    bm = BlockSpaceManager(16, 10)
+    s = Sequence.of_length("a", 40, 16)     # 3 pages
+    assert bm.can_allocate(s)
+    bm.allocate(s)
+    assert bm.get_block_table(s) == [9, 8, 7]
+    bm.free(s)
+    assert bm.get_num_free_gpu_blocks() == 10
+    assert not bm.is_allocated(s)
+    bm.free(s)                              # already freed: no-op
+
+
+def test_remap_matches_oracle():
+    for m in range(0, 6):
+        for n in range(0, 5):
+            assert remap_dst_table(list(range(m)), n) == orc.remap_dst_table(list(range(m)), n)
+
+
+def test_plan_batch_against_oracle():
+    rng = np.random.default_rng(1)
+    src_tables = [rng.permutation(100)[:k].tolist() for k in (5, 1, 12)]
+    dst_pages = [5, 2, 13]                  # n, n+1, n+1
+    alloc = BlockAllocator(16, 40)
+    plan = plan_batch(src_tables, 100, alloc, dst_pages)
+    ref = orc.BlockAllocator(40)
+    ids = []
+    for t, m in zip(src_tables, dst_pages):
+        table = orc.allocate_table(ref, m)
+        ids += orc.remap_dst_table(table, len(t))
+    assert plan.dst_ids == ids
+    assert plan.src_ids == sum(src_tables, [])
+    assert plan.indptr == [0, 5, 6, 18]
+    assert [len(t) for t in plan.dst_tables] == dst_pages
+    assert alloc.free_blocks == ref.free_blocks
+
+
+def test_plan_batch_rejects_without_allocating():
+    alloc = BlockAllocator(16, 4)
+    with pytest.raises(ValueError):
+        plan_batch([[0, 1], [2, 3, 4]], 10, alloc)          # needs 5 > 4
+    assert alloc.get_num_free_blocks() == 4
+    with pytest.raises(ValueError):
+        plan_batch([[0, 1]], 10, alloc, [4])                 # n+2
+    with pytest.raises(IndexError):
+        plan_batch([[10]], 10, alloc)
+    assert alloc.get_num_free_blocks() == 4
+
+
+def test_normalize_and_dedup_follow_torch_semantics():
+    assert normalize_page_ids([0, -1, 3], 4) == [0, 3, 3]
+    with pytest.raises(IndexError):
+        normalize_page_ids([4], 4)
+    with pytest.raises(IndexError):
+        normalize_page_ids([-5], 4)
+    ids = [2, 0, 2, 1, 0]
+    keep = dedup_keep_last(ids)
+    pos, kept = orc.dedup_keep_last(ids, 4)
+    assert keep == pos.tolist() and [ids[p] for p in keep] == kept.tolist()
+
+
+def test_chunk_layers():
+    assert chunk_layers(32, 64 << 20) == 1
+    assert chunk_layers(32, 2 << 20) == 8        # at least 4 chunks
+    assert chunk_layers(32, 512 << 20) == 1
+    assert chunk_layers(1, 1) == 1
+
+
+class _FakeHelper:
+    """Records insert calls; stands in for the device work."""
+
+    def __init__(self):
+        self.calls = []
+
+    def insert_kv_cache(self, content, ids, device):
+        self.calls.append(list(ids))
+        return content.shape[1] == len(ids) or content.shape[1] == 1
+
+    def get_kv_cache(self, seq, seq_manager):
+        return "payload", seq_manager._get_block_table(seq)
+
+
+class _Content:
+    def __init__(self, n):
+        self.shape = (2, n)
+
+    def element_size(self):
+        return 2
+
+    def numel(self):
+        return 2 * self.shape[1]
+
+
+@pytest.mark.parametrize("tokens,src_pages,expect_ids", [
+    (40, 3, [9, 8, 7]),          # n pages on both sides
+    (49, 3, [9, 8, 7]),          # destination has n+1: last page untouched
+])
+def test_worker_insert_remaps_like_reference(tokens, src_pages, expect_ids):
+    helper = _FakeHelper()
+    worker = KVWorker(helper, WorkerSequenceManager(16, 10))
+    seq = Sequence.of_length("r", tokens, 16)
+    kv = KVobj("r", _Content(src_pages), list(range(src_pages)))
+    st = worker._insert_kv_cache(seq, kv, "cuda:0")
+    assert isinstance(st, KVStatus) and st.status
+    assert helper.calls == [expect_ids]
+    assert st.allocate_time >= 0 and st.insertion_time >= 0
+
+
+def test_worker_insert_without_room_returns_false():
+    worker = KVWorker(_FakeHelper(), WorkerSequenceManager(16, 2))
+    seq = Sequence.of_length("r", 40, 16)
+    assert worker._insert_kv_cache(seq, KVobj("r", _Content(3), [0, 1, 2]), 0) is False
+    assert not worker.seq_manager.block_manager.is_allocated(seq)
+
+
+def test_worker_get_frees_source_pages():
+    sm = WorkerSequenceManager(16, 10)
+    worker = KVWorker(_FakeHelper(), sm)
+    seq = Sequence.of_length("r", 20, 16)
+    sm.add_seq(seq)
+    sm.block_manager.allocate(seq)
+    payload, ids, rank = worker._get_kv_cache_nofree(seq)
+    assert ids == [9, 8] and rank == 0
+    assert sm.block_manager.get_num_free_gpu_blocks() == 8
+    worker._get_kv_cache(seq)
+    assert sm.block_manager.get_num_free_gpu_blocks() == 10
+    assert "r" not in sm.seq_map
+
+
+def test_kvobj_size_in_megabytes():
+    import torch
+    t = torch.zeros(2, 3, 2, 16, 8, 128, dtype=torch.float16)
+    assert KVobj("x", t, [0, 1, 2]).size == t.numel() * 2 / 1e6
