@@ -55,6 +55,8 @@ def parse_args():
     ap.add_argument("--no-promote", action="store_true")
     ap.add_argument("--verify", action="store_true", help="check the result against torch's gather/scatter")
     ap.add_argument("--cpu-layers", type=int, default=0, help="layers in the CPU sample (0 = auto)")
+    ap.add_argument("--staging", action="store_true",
+                    help="also time the pinned-host round trip (default for workloads 3 and 4)")
     return ap.parse_args()
 
 
@@ -153,12 +155,57 @@ def run_device(args, w, dev, src, dst, plan, s_ids, d_ids):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "page_copy_kernel<8,false> (pack and unpack launches)",
+            "kernel": "page_copy_kernel<false> (pack and unpack launches)",
             "algorithmic_bytes_per_launch": int(statistics.mean(bytes_per_launch)),
             "mean_launch_us": round(statistics.mean(durs) * 1e3, 2),
         },
     }
     return res
+
+
+def run_staging(w, dev, src, dst, s_ids, d_ids, reps: int = 3):
+    """Pinned-host legs: pack_to_host, unpack_from_host and the overlapped
+    round trip, in GB/s per direction against the PCIe Gen5 x16 peak."""
+    import torch
+
+    from paceserve_amd.kv_transfer import kv_utils, ops
+
+    L, n, pb = w.shape.num_layers, s_ids.numel(), w.shape.page_bytes
+    layer_bytes = n * pb
+    k = w.layers_per_chunk or kv_utils.chunk_layers(L, layer_bytes)
+    chunk = k * layer_bytes
+    chunks = -(-L // k)
+    # host ring of up to 4 chunk regions (a full copy for short payloads)
+    host_bytes = min(w.payload_bytes, 4 * chunk)
+    host = torch.empty(host_bytes, dtype=torch.uint8, pin_memory=True)
+    full = None
+    if w.payload_bytes <= (8 << 30):
+        full = torch.empty((L, n) + w.shape.page_shape, dtype=w.shape.dtype, pin_memory=True)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    out = {"layers_per_chunk": k, "chunks": chunks, "chunk_bytes": chunk, "host_ring_bytes": host_bytes,
+           "pcie_peak_gbs_per_direction": 64.0}
+    with ops.Stager(-(-chunk // 256) * 256, 3, dev) as st:
+        t_rt = timed(lambda: st.roundtrip(src, s_ids, dst, d_ids, host, k))
+        out["roundtrip_ms"] = round(t_rt * 1e3, 3)
+        out["roundtrip_gbs_per_direction"] = round(w.payload_bytes / t_rt / 1e9, 2)
+        if full is not None:
+            t_d2h = timed(lambda: st.pack_to_host(src, s_ids, full, k))
+            t_h2d = timed(lambda: st.unpack_from_host(full, dst, d_ids, k))
+            out["pack_to_host_gbs"] = round(w.payload_bytes / t_d2h / 1e9, 2)
+            out["unpack_from_host_gbs"] = round(w.payload_bytes / t_h2d / 1e9, 2)
+    log(f"staging: round trip {out['roundtrip_ms']} ms = {out['roundtrip_gbs_per_direction']} GB/s per direction")
+    return out
 
 
 def verify(w, src, dst, s_ids, d_ids, dev) -> bool:
@@ -263,6 +310,10 @@ def main():
     _native.load()
     dev = torch.device("cuda", 0)
     w = workloads.config(args.workload)
+    promote = None
+    if not args.no_promote:
+        promote = run_promote(dev)
+        torch.cuda.empty_cache()
     log(f"workload {w.name}: {w.description}")
     src, dst, plan, s_ids, d_ids = device_setup(w, dev)
     res = run_device(args, w, dev, src, dst, plan, s_ids, d_ids)
@@ -277,11 +328,13 @@ def main():
         log(f"CPU baseline on {os.cpu_count()} cores, {layers} layers ...")
         cpu = run_cpu_baseline(w, layers, src, dst, plan)
         log(f"CPU baseline: {cpu['value']} GB/s")
+    staging = None
+    if args.staging or w.staging in ("pinned", "both"):
+        staging = run_staging(w, dev, src, dst, s_ids, d_ids)
+        if args.verify:
+            res["verified_after_staging"] = verify(w, src, dst, s_ids, d_ids, dev)
     del src, dst, s_ids, d_ids
     torch.cuda.empty_cache()
-    promote = None
-    if not args.no_promote:
-        promote = run_promote(dev)
 
     line = {
         "metric": METRIC,
@@ -303,10 +356,12 @@ def main():
         "unpack_ms": res["unpack_ms_mean"],
         "roofline": res["roofline"],
         "promote_4k": promote,
+        "staging": staging,
         "cpu_baseline": cpu,
     }
-    if "verified" in res:
-        line["verified"] = res["verified"]
+    for key in ("verified", "verified_after_staging"):
+        if key in res:
+            line[key] = res[key]
     print(json.dumps(line), flush=True)
 
 
