@@ -55,6 +55,8 @@ def parse_args():
     ap.add_argument("--no-promote", action="store_true")
     ap.add_argument("--verify", action="store_true", help="check the result against torch's gather/scatter")
     ap.add_argument("--cpu-layers", type=int, default=0, help="layers in the CPU sample (0 = auto)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="after timing, run torch's contiguous copy of 1 GiB three times (PMC scale reference)")
     ap.add_argument("--staging", action="store_true",
                     help="also time the pinned-host round trip (default for workloads 3 and 4)")
     return ap.parse_args()
@@ -84,7 +86,7 @@ def run_device(args, w, dev, src, dst, plan, s_ids, d_ids):
 
     L = w.shape.num_layers
     n = plan.n_pages
-    k = w.layers_per_chunk or L
+    k = w.device_layers_per_chunk or L
     buf = torch.empty((min(k, L), n) + w.shape.page_shape, dtype=w.shape.dtype, device=dev)
     stream = torch.cuda.current_stream(dev)
 
@@ -161,6 +163,39 @@ def run_device(args, w, dev, src, dst, plan, s_ids, d_ids):
         },
     }
     return res
+
+
+def run_ceiling(w, dev, src, dst, n: int, reps: int = 10) -> dict:
+    """The same kernel with identity page ids (pages 0..n-1 of each pool, so
+    both sides are contiguous): the device's copy ceiling for this kernel and
+    payload, measured beside the indexed run."""
+    import torch
+
+    from paceserve_amd.kv_transfer import ops
+
+    L = w.shape.num_layers
+    k = w.device_layers_per_chunk or L
+    ids = torch.arange(n, dtype=torch.int32, device=dev)
+    buf = torch.empty((min(k, L), n) + w.shape.page_shape, dtype=w.shape.dtype, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        for lb in range(0, L, k):
+            le = min(L, lb + k)
+            ops.pack(src, ids, buf[: le - lb], layer_begin=lb, layer_end=le)
+            ops.unpack(buf[: le - lb], dst, ids, layer_begin=lb, layer_end=le)
+
+    step()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        step()
+    b.record(stream)
+    torch.cuda.synchronize()
+    gbs = 4 * w.payload_bytes * reps / (a.elapsed_time(b) / 1e3) / 1e9
+    log(f"contiguous ceiling (identity ids): {gbs:.1f} GB/s")
+    return {"identity_ids_gbs": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def run_staging(w, dev, src, dst, s_ids, d_ids, reps: int = 3):
@@ -258,6 +293,33 @@ def run_promote(dev, steps=100, warmup=10):
     return out
 
 
+def cpu_sample_layers(w) -> int:
+    """Layers in the CPU sample: up to 16, within 64 GiB and half of the host's
+    free memory (two host pools plus the buffer per layer)."""
+    try:
+        import psutil
+        free = psutil.virtual_memory().available
+    except ImportError:
+        free = 32 << 30
+    per_layer = (w.src_pool_pages + w.dst_pool_pages + w.n_pages) * w.shape.page_bytes
+    budget = min(64 << 30, int(0.5 * free))
+    return max(1, min(w.shape.num_layers, budget // per_layer, 16))
+
+
+def run_calibration(dev) -> None:
+    """torch's contiguous device copy of 1 GiB, three times: the reference
+    dispatch whose FETCH_SIZE / WRITE_SIZE counters scale ours to bytes."""
+    import torch
+
+    a = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log("calibration: 3 x 1 GiB torch copy_ done")
+
+
 def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan):
     """The reference's CPU path on pageable host tensors: per layer,
     index_select into the buffer then index_copy_ into the destination.  The
@@ -275,9 +337,12 @@ def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan):
     s_idx = torch.tensor(plan.src_ids, dtype=torch.long)
     d_idx = torch.tensor(plan.dst_ids, dtype=torch.long)
     buf = torch.empty((L, plan.n_pages) + w.shape.page_shape, dtype=w.shape.dtype)
+    t0 = time.perf_counter()
     orc.torch_cpu_pack_unpack(src, s_idx, dst, d_idx, buf)            # warm-up
+    first = time.perf_counter() - t0
+    reps = int(min(50, max(5, 10.0 // max(first, 1e-3))))            # ~10 s of CPU work
     times = []
-    for _ in range(5):
+    for _ in range(reps):
         t0 = time.perf_counter()
         orc.torch_cpu_pack_unpack(src, s_idx, dst, d_idx, buf)
         times.append(time.perf_counter() - t0)
@@ -289,13 +354,64 @@ def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan):
         "cores": cores,
         "kind": "port",
         "sample": f"{L} of {w.shape.num_layers} layers, all {plan.n_pages} pages of {w.name} "
-                  f"({payload / 2**30:.2f} GiB payload), full-size pools per layer; median of 5 "
+                  f"({payload / 2**30:.2f} GiB payload), full-size pools per layer; median of {reps} "
                   f"after 1 warm-up; torch {torch.__version__} index_select/index_copy_ on host tensors",
         "seconds_per_pass": round(t, 4),
     }
 
 
+PROFILES = ROOT / "profiles"
+KERNEL_TAG = "page_copy_kernel<false>"
+
+
+def _per_dispatch(csv_path: str, counter: str):
+    import csv
+
+    by = {}
+    for r in csv.DictReader(open(csv_path)):
+        if r["Counter_Name"] != counter:
+            continue
+        by.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return by
+
+
+def summarize_pmc(fetch_csv: str, write_csv: str, workload: str) -> dict:
+    """HBM bytes per copy-kernel launch from two rocprofv3 --pmc runs
+    (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled so that the 1 GiB
+    device copy run by --calibrate (dispatched as __amd_rocclr_copyBuffer)
+    reads 1 GiB fetched and 1 GiB written."""
+    gib_kib = float(1 << 20)
+    out = {"workload": workload, "kernel": KERNEL_TAG}
+    for name, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"), ("write", write_csv, "WRITE_SIZE")):
+        by = _per_dispatch(path, counter)
+        ours = [v for k, vals in by.items() if "page_copy_kernel" in k for v in vals]
+        calib = [v for k, vals in by.items() if "copyBuffer" in k for v in vals if v > 0.25 * gib_kib]
+        if not ours or not calib:
+            raise SystemExit(f"{path}: missing page_copy_kernel or calibration dispatches")
+        factor = gib_kib / statistics.mean(calib)
+        out[f"{name}_kib_per_dispatch_raw"] = statistics.mean(ours)
+        out[f"{name}_calibration_kib_raw"] = statistics.mean(calib)
+        out[f"{name}_scale"] = round(factor, 4)
+        out[f"{name}_bytes_per_launch"] = int(statistics.mean(ours) * factor * 1024)
+        out[f"{name}_dispatches"] = len(ours)
+    out["traffic_bytes_per_launch"] = out["fetch_bytes_per_launch"] + out["write_bytes_per_launch"]
+    return out
+
+
+def traffic_from_profiles(workload: str):
+    path = PROFILES / f"page_copy_{workload}_traffic.json"
+    if not path.exists():
+        return None
+    d = json.loads(path.read_text())
+    return d if d.get("workload") == workload else None
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-pmc":
+        # python bench.py --summarize-pmc FETCH.csv WRITE.csv WORKLOAD
+        d = summarize_pmc(sys.argv[2], sys.argv[3], sys.argv[4])
+        print(json.dumps(d, indent=1))
+        return
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -322,9 +438,12 @@ def main():
     if args.verify:
         res["verified"] = verify(w, src, dst, s_ids, d_ids, dev)
         log(f"verified: {res['verified']}")
+    ceiling = run_ceiling(w, dev, src, dst, plan.n_pages) if args.mode == "buffer" else None
+    if args.calibrate:
+        run_calibration(dev)
     cpu = None
     if not args.no_cpu:
-        layers = args.cpu_layers or max(1, min(w.shape.num_layers, 8))
+        layers = args.cpu_layers or cpu_sample_layers(w)
         log(f"CPU baseline on {os.cpu_count()} cores, {layers} layers ...")
         cpu = run_cpu_baseline(w, layers, src, dst, plan)
         log(f"CPU baseline: {cpu['value']} GB/s")
@@ -355,10 +474,15 @@ def main():
         "pack_ms": res["pack_ms_mean"],
         "unpack_ms": res["unpack_ms_mean"],
         "roofline": res["roofline"],
+        "copy_ceiling": ceiling,
         "promote_4k": promote,
         "staging": staging,
         "cpu_baseline": cpu,
     }
+    tr = traffic_from_profiles(w.name) if args.mode == "buffer" else None
+    if tr is not None:
+        line["roofline"]["traffic"] = tr["traffic_bytes_per_launch"]
+        line["roofline"]["traffic_source"] = f"profiles/page_copy_{w.name}_traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)"
     for key in ("verified", "verified_after_staging"):
         if key in res:
             line[key] = res[key]

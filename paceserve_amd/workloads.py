@@ -63,7 +63,8 @@ class Workload:
     seed: int
     init: str = "normal"             # "normal" = N(0,1), "uniform4" = U[-4, 4]
     staging: str = "device"          # "device", "pinned" or "both"
-    layers_per_chunk: Optional[int] = None
+    layers_per_chunk: Optional[int] = None         # host-leg (staging) chunk
+    device_layers_per_chunk: Optional[int] = None  # transfer-buffer chunk on device
     dst_free: Optional[List[int]] = None
     notes: dict = field(default_factory=dict)
 
@@ -171,7 +172,7 @@ def config(c) -> Workload:
                     k += 1
         return Workload("config5", "256 requests U{64..2048} tokens, Llama-3-70B KV (80 layers), bf16, "
                         "20480-page pools dealt round-robin (heavily fragmented), 8-layer chunks",
-                        shape, 20480, 20480, lengths, tables, seed, layers_per_chunk=8)
+                        shape, 20480, 20480, lengths, tables, seed, device_layers_per_chunk=8)
     if c == "promote4k":
         seed = 1100
         rng = np.random.default_rng(seed)

@@ -1,0 +1,147 @@
+"""The five reference-shaped workloads at full size on the GPU.
+
+For each: plan (LIFO destination allocation + remap), move the pages through
+the HIP path, then check
+  - every destination page equals its source page (torch's own device gather
+    of both sides, compared as raw words);
+  - untouched destination pages and the whole source pool are unchanged: a
+    checksum of per-layer word sums must move by exactly the touched pages'
+    contribution (sum_after = sum_before - old touched pages + new pages);
+  - config 1 additionally against the CPU oracle, config 2 additionally
+    against an exact torch index_copy_ of a clone of the destination pool,
+    configs 3 and 4 also through the pinned-host round trip.
+"""
+import gc
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as orc
+from paceserve_amd import workloads
+from paceserve_amd.core.block_manager import BlockAllocator
+from paceserve_amd.kv_transfer import migrate, ops
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _free_memory():
+    yield
+    gc.collect()
+    if torch.cuda.is_available():
+        torch.cuda.empty_cache()
+
+
+def words(t):
+    return t.view(torch.int16)
+
+
+def layer_sum(t):
+    return int(words(t).sum(dtype=torch.int64).item())
+
+
+def pages_sum(t, ids):
+    return int(words(t).index_select(0, ids).sum(dtype=torch.int64).item())
+
+
+def setup(c, dev):
+    w = workloads.config(c)
+    free_gb = torch.cuda.mem_get_info(dev)[0] / 1e9
+    need_gb = (w.src_pool_pages + w.dst_pool_pages) * w.shape.num_layers * w.shape.page_bytes / 1e9
+    if need_gb > 0.9 * free_gb:
+        pytest.skip(f"{w.name} needs {need_gb:.0f} GB of device memory, {free_gb:.0f} GB free")
+    src = ops.PagedPool(workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev))
+    dst = ops.PagedPool(workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev))
+    plan = migrate.plan_batch(w.src_tables, w.src_pool_pages, BlockAllocator(16, w.dst_pool_pages))
+    s_ids = torch.tensor(plan.src_ids, dtype=torch.long, device=dev)
+    d_ids = torch.tensor(plan.dst_ids, dtype=torch.long, device=dev)
+    return w, src, dst, plan, s_ids, d_ids
+
+
+def sums_before(src, dst, s_ids, d_ids):
+    return ([layer_sum(t) for t in src.layers], [layer_sum(t) for t in dst.layers],
+            [pages_sum(t, d_ids) for t in dst.layers], [pages_sum(t, s_ids) for t in src.layers])
+
+
+def check_after(src, dst, s_ids, d_ids, before, label):
+    src_all, dst_all, dst_touched, src_sel = before
+    for l in range(src.num_layers):
+        a = words(src.layers[l]).index_select(0, s_ids)
+        b = words(dst.layers[l]).index_select(0, d_ids)
+        assert torch.equal(a, b), f"{label}: layer {l} destination pages differ from source pages"
+        assert layer_sum(src.layers[l]) == src_all[l], f"{label}: layer {l} source pool written"
+        assert layer_sum(dst.layers[l]) == dst_all[l] - dst_touched[l] + src_sel[l], \
+            f"{label}: layer {l} untouched destination pages changed"
+
+
+def run_buffer(w, src, dst, plan, dev):
+    mig = migrate.KVMigrator(src, dst, BlockAllocator(16, w.dst_pool_pages))
+    s32 = torch.tensor(plan.src_ids, dtype=torch.int32, device=dev)
+    d32 = torch.tensor(plan.dst_ids, dtype=torch.int32, device=dev)
+    mig.move_pages(s32, d32, "buffer", w.device_layers_per_chunk)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("c", [1, 2, 3, 4, 5])
+def test_workload_buffer_path(gpu, c):
+    w, src, dst, plan, s_ids, d_ids = setup(c, gpu)
+    print(f"{w.name}: {plan.n_pages} pages x {w.shape.num_layers} layers", flush=True)
+    before = sums_before(src, dst, s_ids, d_ids)
+    exact = None
+    if c == 2:      # exact expected destination for one layer set
+        exact = [words(d).clone().index_copy_(0, d_ids, words(s).index_select(0, s_ids))
+                 for s, d in zip(src.layers[:4], dst.layers[:4])]
+    if c == 1:      # CPU oracle on the full (small) workload
+        np_src = [words(s).cpu().numpy() for s in src.layers]
+        np_dst = [words(d).cpu().numpy() for d in dst.layers]
+        want = orc.move(np_src, plan.src_ids, np_dst, plan.dst_ids)
+    run_buffer(w, src, dst, plan, gpu)
+    check_after(src, dst, s_ids, d_ids, before, w.name)
+    if exact is not None:
+        for l in range(4):
+            assert torch.equal(words(dst.layers[l]), exact[l]), f"layer {l} differs from index_copy_"
+    if c == 1:
+        for l in range(w.shape.num_layers):
+            np.testing.assert_array_equal(words(dst.layers[l]).cpu().numpy(), want[l])
+
+
+@pytest.mark.parametrize("c", [3, 4])
+def test_workload_pinned_roundtrip(gpu, c):
+    w, src, dst, plan, s_ids, d_ids = setup(c, gpu)
+    before = sums_before(src, dst, s_ids, d_ids)
+    from paceserve_amd.kv_transfer import kv_utils
+    n = plan.n_pages
+    k = w.layers_per_chunk or kv_utils.chunk_layers(w.shape.num_layers, n * w.shape.page_bytes)
+    chunk = k * n * w.shape.page_bytes
+    host = torch.empty(min(w.payload_bytes, 3 * chunk), dtype=torch.uint8, pin_memory=True)
+    with ops.Stager(chunk, 3, gpu) as st:
+        st.roundtrip(src, plan.src_ids, dst, plan.dst_ids, host, k)
+        torch.cuda.synchronize()
+    check_after(src, dst, s_ids, d_ids, before, f"{w.name} pinned")
+
+
+def test_workload_fused_move_matches(gpu):
+    w, src, dst, plan, s_ids, d_ids = setup(2, gpu)
+    before = sums_before(src, dst, s_ids, d_ids)
+    ops.move(src, plan.src_ids, dst, plan.dst_ids)
+    torch.cuda.synchronize()
+    check_after(src, dst, s_ids, d_ids, before, "config2 fused")
+
+
+def test_promote_4k_all_modes(gpu):
+    w = workloads.config("promote4k")
+    src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, gpu)
+    outs = {}
+    for mode in ("buffer", "fused", "pinned"):
+        dst = workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, gpu)
+        alloc = BlockAllocator(16, w.dst_pool_pages)
+        mig = migrate.KVMigrator(src, dst, alloc)
+        plan = mig.promote(w.src_tables, mode=mode)
+        torch.cuda.synchronize()
+        assert plan.dst_tables == [list(range(2047, 2047 - 256, -1))]    # fresh LIFO pool
+        outs[mode] = [words(d).clone() for d in dst]
+        del dst, mig
+    for mode in ("fused", "pinned"):
+        for l in range(w.shape.num_layers):
+            assert torch.equal(outs[mode][l], outs["buffer"][l]), f"{mode} layer {l}"
