@@ -284,23 +284,26 @@ def run_promote(dev, steps=100, warmup=10):
     import torch
 
     from paceserve_amd import workloads
-    from paceserve_amd.core.block_manager import BlockAllocator
+    from paceserve_amd.core.block_manager import BlockAllocator, NativeBlockAllocator
     from paceserve_amd.kv_transfer import migrate
 
     w = workloads.config("promote4k")
     src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev)
     dst = workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev)
-    alloc = BlockAllocator(w.shape.page_size, w.dst_pool_pages)
-    mig = migrate.KVMigrator(src, dst, alloc)
     host = torch.empty(w.payload_bytes, dtype=torch.uint8, pin_memory=True)
     out = {}
-    for mode in ("buffer", "fused", "pinned"):
+    # "buffer"/"fused": Python planner + ops; "*_native": one pace_kv_promote call
+    for mode in ("buffer", "fused", "pinned", "buffer_native", "fused_native"):
+        native = mode.endswith("_native")
+        alloc = (NativeBlockAllocator if native else BlockAllocator)(w.shape.page_size, w.dst_pool_pages)
+        mig = migrate.KVMigrator(src, dst, alloc)
+        kind = mode.replace("_native", "")
         lat = []
         n_iter = warmup + (steps if mode != "pinned" else max(20, steps // 5))
         for i in range(n_iter):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            plan = mig.promote(w.src_tables, mode=mode, host_buf=host if mode == "pinned" else None)
+            plan = mig.promote(w.src_tables, mode=kind, host_buf=host if kind == "pinned" else None)
             ev = torch.cuda.Event()
             ev.record()
             ev.synchronize()

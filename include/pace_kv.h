@@ -182,6 +182,87 @@ int pace_kv_roundtrip(pace_kv_stager* stager,
                       int layers_per_chunk, void* host_buf, int64_t host_bytes,
                       int32_t* err_count, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Native block allocation, batch planning and single-call promotion          */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * LIFO free list of page ids over [0, num_pages), guarded by a mutex.
+ * free_list NULL means the fresh pool [0, 1, ..., num_pages-1], which hands
+ * out num_pages-1 first; otherwise free_list[free_len-1] is handed out first.
+ *
+ * Replaces BlockAllocator
+ *   (paceserve/core/block_space_manager/base_block_space_manager.py:11-47).
+ */
+typedef struct pace_kv_allocator pace_kv_allocator;
+
+int pace_kv_allocator_create(int64_t num_pages, const int32_t* free_list,
+                             int64_t free_len, pace_kv_allocator** out);
+int pace_kv_allocator_destroy(pace_kv_allocator* alloc);
+int pace_kv_allocator_num_free(pace_kv_allocator* alloc, int64_t* out);
+
+/* n pages in the order n successive pops return them; all-or-nothing:
+ * PACE_KV_ENOMEM ("Out of memory! No free blocks are available.") leaves the
+ * list unchanged.  Replaces BlockAllocator.allocate (:34-39) and
+ * BaseBlockSpaceManager.allocate (:89-97). */
+int pace_kv_allocator_allocate(pace_kv_allocator* alloc, int64_t n, int32_t* out_ids);
+
+/* Returns each distinct page of ids[0..n) once, in first-occurrence order.
+ * Replaces BaseBlockSpaceManager._free_block_table (:119-121). */
+int pace_kv_allocator_free(pace_kv_allocator* alloc, const int32_t* ids, int64_t n);
+
+/* Copies the free list (allocation order: last entry first) into out. */
+int pace_kv_allocator_snapshot(pace_kv_allocator* alloc, int32_t* out,
+                               int64_t capacity, int64_t* len);
+
+/*
+ * Plans a batch of num_requests migrations: request r's source pages are
+ * src_ids[src_indptr[r] .. src_indptr[r+1]) (host arrays, ids in
+ * [0, src_pool_pages)); it receives dst_pages[r] destination pages (NULL:
+ * as many as its source pages), which must be n_r or n_r + 1.  Pages are
+ * allocated request by request from dst_alloc, all-or-nothing.  Outputs (host):
+ * out_dst_tables, every request's full destination table (sum of dst_pages
+ * entries); out_dst_ids, the pages that receive data, CSR like src_ids (a
+ * table of n_r + 1 pages leaves its last page untouched).
+ *
+ * Replaces the destination allocation and remap of BaseWorker._insert_kv_cache
+ * (paceserve/worker/base_worker.py:255-277) for a whole batch.
+ */
+int pace_kv_plan(pace_kv_allocator* dst_alloc, int num_requests,
+                 const int64_t* src_indptr, const int32_t* src_ids,
+                 int64_t src_pool_pages, const int32_t* dst_pages,
+                 int32_t* out_dst_tables, int32_t* out_dst_ids);
+
+/*
+ * A promoter owns two pinned host slots and two device slots for block-table
+ * ids, and the events that guard their reuse.
+ */
+typedef struct pace_kv_promoter pace_kv_promoter;
+
+int pace_kv_promoter_create(pace_kv_promoter** out);
+int pace_kv_promoter_destroy(pace_kv_promoter* promoter);
+
+/*
+ * One-call promotion of a batch: pace_kv_plan, one host-to-device copy of
+ * both id lists on `stream`, then the page movement: with buffer == NULL a
+ * fused pace_kv_move; otherwise pace_kv_pack into `buffer` followed by
+ * pace_kv_unpack, in chunks of buffer_layers layers (the buffer holds
+ * buffer_layers layers of buffer_layer_stride bytes).  out_dst_tables is as in
+ * pace_kv_plan.  On failure no destination page stays allocated.
+ *
+ * Replaces KVhelper.get_kv_cache + BaseWorker._insert_kv_cache for requests
+ * whose source and destination caches share a GPU
+ * (paceserve/worker/base_worker.py:236-281, kv_utils.py:33-56).
+ */
+int pace_kv_promote(pace_kv_promoter* promoter, pace_kv_allocator* dst_alloc,
+                    const void* const* src_layers, int64_t src_pool_pages,
+                    void* const* dst_layers, int64_t dst_pool_pages,
+                    int num_layers, int64_t page_bytes, int num_requests,
+                    const int64_t* src_indptr, const int32_t* src_ids,
+                    const int32_t* dst_pages, void* buffer,
+                    int64_t buffer_layer_stride, int buffer_layers,
+                    int32_t* out_dst_tables, int32_t* err_count, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -6,6 +6,13 @@
 
 #include "pace_kv.h"
 
+// Returns from the enclosing function with the status of `expr` if non-zero.
+#define PACE_KV_TRY(expr)  \
+  do {                     \
+    int rc_ = (expr);      \
+    if (rc_) return rc_;   \
+  } while (0)
+
 namespace pace_kv {
 
 // Records `msg` (printf-style) as the calling thread's last error and returns

@@ -119,13 +119,7 @@ int make_plan(const pace_kv_stager* s, int num_layers, int64_t n_pages, int64_t 
   return PACE_KV_OK;
 }
 
-#define PACE_TRY(expr)      \
-  do {                      \
-    int rc_ = (expr);       \
-    if (rc_) return rc_;    \
-  } while (0)
-
-#define PACE_HIP(expr, what) PACE_TRY(hip_status((expr), (what)))
+#define PACE_HIP(expr, what) PACE_KV_TRY(hip_status((expr), (what)))
 
 // pack(chunk c) of the source pool into out slot `slot`, on `stream`.
 int pack_chunk(pace_kv_stager* s, const ChunkPlan& p, int c, const void* const* src_layers,
@@ -190,16 +184,16 @@ int pace_kv_pack_to_host(pace_kv_stager* s, const void* const* src_layers, int n
                          int64_t pool_pages, const int32_t* page_ids, int64_t n_pages,
                          int64_t page_bytes, int layers_per_chunk, void* host_out,
                          int32_t* err_count, void* stream_) {
-  PACE_TRY(check_stager(s));
+  PACE_KV_TRY(check_stager(s));
   ChunkPlan p;
-  PACE_TRY(make_plan(s, num_layers, n_pages, page_bytes, layers_per_chunk, &p));
+  PACE_KV_TRY(make_plan(s, num_layers, n_pages, page_bytes, layers_per_chunk, &p));
   if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
   if (host_out == nullptr) return fail(PACE_KV_EINVAL, "pack_to_host: host_out is NULL");
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   for (int c = 0; c < p.num_chunks(); ++c) {
     const int slot = c % s->num_slots;
     PACE_HIP(hipStreamWaitEvent(stream, s->out_free[slot], 0), "wait out slot");
-    PACE_TRY(pack_chunk(s, p, c, src_layers, pool_pages, page_ids, err_count, stream));
+    PACE_KV_TRY(pack_chunk(s, p, c, src_layers, pool_pages, page_ids, err_count, stream));
     PACE_HIP(hipEventRecord(s->packed[slot], stream), "record packed");
     PACE_HIP(hipStreamWaitEvent(s->d2h, s->packed[slot], 0), "wait packed");
     PACE_HIP(hipMemcpyAsync(static_cast<char*>(host_out) + p.first(c) * p.layer_bytes,
@@ -217,9 +211,9 @@ int pace_kv_unpack_from_host(pace_kv_stager* s, const void* host_in, void* const
                              int num_layers, int64_t pool_pages, const int32_t* page_ids,
                              int64_t n_pages, int64_t page_bytes, int layers_per_chunk,
                              int32_t* err_count, void* stream_) {
-  PACE_TRY(check_stager(s));
+  PACE_KV_TRY(check_stager(s));
   ChunkPlan p;
-  PACE_TRY(make_plan(s, num_layers, n_pages, page_bytes, layers_per_chunk, &p));
+  PACE_KV_TRY(make_plan(s, num_layers, n_pages, page_bytes, layers_per_chunk, &p));
   if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
   if (host_in == nullptr) return fail(PACE_KV_EINVAL, "unpack_from_host: host_in is NULL");
   hipStream_t stream = static_cast<hipStream_t>(stream_);
@@ -235,7 +229,7 @@ int pace_kv_unpack_from_host(pace_kv_stager* s, const void* host_in, void* const
              "H2D copy");
     PACE_HIP(hipEventRecord(s->in_ready[slot], s->h2d), "record in_ready");
     PACE_HIP(hipStreamWaitEvent(stream, s->in_ready[slot], 0), "wait in_ready");
-    PACE_TRY(unpack_chunk(s, p, c, dst_layers, pool_pages, page_ids, err_count, stream));
+    PACE_KV_TRY(unpack_chunk(s, p, c, dst_layers, pool_pages, page_ids, err_count, stream));
     PACE_HIP(hipEventRecord(s->in_free[slot], stream), "record in_free");
   }
   return PACE_KV_OK;
@@ -246,9 +240,9 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
                       const int32_t* dst_ids, int num_layers, int64_t n_pages, int64_t page_bytes,
                       int layers_per_chunk, void* host_buf, int64_t host_bytes,
                       int32_t* err_count, void* stream_) {
-  PACE_TRY(check_stager(s));
+  PACE_KV_TRY(check_stager(s));
   ChunkPlan p;
-  PACE_TRY(make_plan(s, num_layers, n_pages, page_bytes, layers_per_chunk, &p));
+  PACE_KV_TRY(make_plan(s, num_layers, n_pages, page_bytes, layers_per_chunk, &p));
   if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
   if (host_buf == nullptr) return fail(PACE_KV_EINVAL, "roundtrip: host_buf is NULL");
   const int64_t chunk_bytes = p.layer_bytes * p.layers_per_chunk;
@@ -272,7 +266,7 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
   auto issue_unpack = [&](int c) -> int {
     const int slot = c % s->num_slots;
     PACE_HIP(hipStreamWaitEvent(stream, s->in_ready[slot], 0), "wait in_ready");
-    PACE_TRY(unpack_chunk(s, p, c, dst_layers, dst_pool_pages, dst_ids, err_count, stream));
+    PACE_KV_TRY(unpack_chunk(s, p, c, dst_layers, dst_pool_pages, dst_ids, err_count, stream));
     PACE_HIP(hipEventRecord(s->in_free[slot], stream), "record in_free");
     return PACE_KV_OK;
   };
@@ -282,7 +276,7 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
     char* region = host + static_cast<int64_t>(r) * chunk_bytes;
     const int64_t bytes = p.count(c) * p.layer_bytes;
     PACE_HIP(hipStreamWaitEvent(stream, s->out_free[slot], 0), "wait out slot");
-    PACE_TRY(pack_chunk(s, p, c, src_layers, src_pool_pages, src_ids, err_count, stream));
+    PACE_KV_TRY(pack_chunk(s, p, c, src_layers, src_pool_pages, src_ids, err_count, stream));
     PACE_HIP(hipEventRecord(s->packed[slot], stream), "record packed");
     PACE_HIP(hipStreamWaitEvent(s->d2h, s->packed[slot], 0), "wait packed");
     PACE_HIP(hipStreamWaitEvent(s->d2h, s->host_free[r], 0), "wait host region");
@@ -294,7 +288,7 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
     // unpack(c - kLag) last reads in slot (c - kLag) % num_slots; it must be
     // enqueued before H2D(c) waits on in_free of slot c % num_slots, which is
     // the same slot when num_slots == kLag.
-    if (c - kLag >= next_unpack) PACE_TRY(issue_unpack(next_unpack++));
+    if (c - kLag >= next_unpack) PACE_KV_TRY(issue_unpack(next_unpack++));
     PACE_HIP(hipStreamWaitEvent(s->h2d, s->host_full[r], 0), "wait host_full");
     PACE_HIP(hipStreamWaitEvent(s->h2d, s->in_free[slot], 0), "wait in slot");
     PACE_HIP(hipMemcpyAsync(s->in_ring + slot * s->slot_bytes, region, bytes,
@@ -303,7 +297,7 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
     PACE_HIP(hipEventRecord(s->in_ready[slot], s->h2d), "record in_ready");
     PACE_HIP(hipEventRecord(s->host_free[r], s->h2d), "record host_free");
   }
-  while (next_unpack < chunks) PACE_TRY(issue_unpack(next_unpack++));
+  while (next_unpack < chunks) PACE_KV_TRY(issue_unpack(next_unpack++));
   return PACE_KV_OK;
 }
 

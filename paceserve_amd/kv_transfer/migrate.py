@@ -28,7 +28,7 @@ from typing import List, Optional, Sequence
 
 import torch
 
-from ..core.block_manager import BlockAllocator, remap_dst_table
+from ..core.block_manager import BlockAllocator, NativeBlockAllocator, remap_dst_table
 from . import ops
 from .kv_utils import normalize_page_ids
 
@@ -90,6 +90,7 @@ class KVMigrator:
         self.buffer_bytes_max = int(buffer_bytes_max)
         self.stager = stager
         self._buf: Optional[torch.Tensor] = None
+        self._promoter: Optional[ops.Promoter] = None
 
     # ------------------------------------------------------------ planning
 
@@ -151,11 +152,47 @@ class KVMigrator:
         else:
             raise ValueError(f"unknown mode {mode!r}")
 
+    def promote_native(self, src_ids, indptr, dst_pages=None, mode: str = "fused",
+                       layers_per_chunk: Optional[int] = None):
+        """One library call (pace_kv_promote) for a CSR batch: src_ids int32
+        (ids in [0, num_pages)), indptr int64.  Needs a NativeBlockAllocator.
+        Returns the destination tables concatenated (int32 array)."""
+        if not isinstance(self.dst_allocator, NativeBlockAllocator):
+            raise TypeError("promote_native needs a NativeBlockAllocator")
+        if self._promoter is None:
+            self._promoter = ops.Promoter(self.src.device)
+        buf = None
+        if mode == "buffer":
+            n = int(indptr[-1])
+            k = layers_per_chunk or self.chunk_layers(n)
+            buf = self._buffer(min(k, self.src.num_layers), n)
+        elif mode != "fused":
+            raise ValueError(f"promote_native supports modes 'buffer' and 'fused', not {mode!r}")
+        return self._promoter.promote(self.src, self.dst, self.dst_allocator, src_ids, indptr,
+                                      dst_pages, buf)
+
     def promote(self, src_tables: Sequence[Sequence[int]], dst_pages: Optional[Sequence[int]] = None,
                 mode: str = "buffer", layers_per_chunk: Optional[int] = None,
                 host_buf: Optional[torch.Tensor] = None) -> MigrationPlan:
         """Plans, uploads and moves a batch of requests; returns the plan.  The
-        work is enqueued on the current stream (synchronize to wait)."""
+        work is enqueued on the current stream (synchronize to wait).  With a
+        NativeBlockAllocator, the device modes run as one library call."""
+        if isinstance(self.dst_allocator, NativeBlockAllocator) and mode in ("buffer", "fused"):
+            import numpy as np
+            counts = [len(t) for t in src_tables]
+            indptr = np.zeros(len(counts) + 1, dtype=np.int64)
+            np.cumsum(counts, out=indptr[1:])
+            src_flat = [i for t in src_tables for i in normalize_page_ids(t, self.src.num_pages)]
+            src_ids = np.array(src_flat, dtype=np.int32)
+            tables = self.promote_native(src_ids, indptr, dst_pages, mode, layers_per_chunk)
+            sizes = counts if dst_pages is None else list(dst_pages)
+            dst_tables, dst_ids, pos = [], [], 0
+            for n, m in zip(counts, sizes):
+                t = tables[pos:pos + m].tolist()
+                pos += m
+                dst_tables.append(t)
+                dst_ids.extend(t[:n])
+            return MigrationPlan(src_flat, dst_ids, dst_tables, indptr.tolist())
         plan = self.plan(src_tables, dst_pages)
         if plan.n_pages:
             s_ids, d_ids = self.upload(plan)

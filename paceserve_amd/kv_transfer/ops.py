@@ -180,6 +180,63 @@ def move(src, src_ids: IdsLike, dst, dst_ids: IdsLike, *, layer_begin: int = 0,
         d_ids.data_ptr(), le - lb, n, sp.page_bytes, _err_ptr(err), _stream_handle(sp.device)))
 
 
+class Promoter:
+    """pace_kv_promoter: plans a batch on a NativeBlockAllocator, uploads both
+    id lists with one copy and moves the pages, all in one library call."""
+
+    def __init__(self, device: Optional[torch.device] = None):
+        self.device = torch.device(device) if device is not None else torch.device(
+            "cuda", torch.cuda.current_device())
+        handle = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            _native.check(_native.load().pace_kv_promoter_create(ctypes.byref(handle)))
+        self._handle = handle.value
+
+    def promote(self, src, dst, allocator, src_ids, indptr, dst_pages=None,
+                buffer: Optional[torch.Tensor] = None, err: Optional[torch.Tensor] = None):
+        """Returns every request's destination table, concatenated (int32
+        numpy array; request r owns dst_pages[r] entries)."""
+        import numpy as np
+
+        sp, dp = as_pool(src), as_pool(dst)
+        if not sp.compatible(dp) or sp.num_layers != dp.num_layers:
+            raise ValueError("source and destination pools differ in layout, layers, dtype or device")
+        if self._handle is None:
+            raise RuntimeError("promoter is closed")
+        src_ids = np.ascontiguousarray(src_ids, dtype=np.int32)
+        indptr = np.ascontiguousarray(indptr, dtype=np.int64)
+        counts = np.diff(indptr) if dst_pages is None else np.ascontiguousarray(dst_pages, dtype=np.int32)
+        total = int(counts.sum())
+        tables = np.empty(max(total, 1), dtype=np.int32)
+        buf_ptr, stride, blayers = None, 0, 0
+        if buffer is not None:
+            stride = _check_buffer(buffer, sp, 1, src_ids.size, "promote")
+            buf_ptr, blayers = buffer.data_ptr(), int(buffer.shape[0])
+        rc = _native.load().pace_kv_promote(
+            self._handle, allocator.handle, sp.table(), sp.num_pages, dp.table(), dp.num_pages,
+            sp.num_layers, sp.page_bytes, indptr.size - 1, indptr.ctypes.data,
+            src_ids.ctypes.data if src_ids.size else None,
+            None if dst_pages is None else counts.ctypes.data, buf_ptr, stride, blayers,
+            tables.ctypes.data, _err_ptr(err), _stream_handle(sp.device))
+        if rc == _native.PACE_KV_ENOMEM:
+            from ..core.block_manager import OOM_MESSAGE
+            raise ValueError(OOM_MESSAGE)
+        _native.check(rc)
+        return tables[:total]
+
+    def close(self) -> None:
+        if self._handle is not None:
+            handle, self._handle = self._handle, None
+            with torch.cuda.device(self.device):
+                _native.check(_native.load().pace_kv_promoter_destroy(handle))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Stager:
     """Pinned-host staging pipeline (pace_kv_stager): device slot rings, a D2H
     and an H2D side stream, and the events that order them.
