@@ -316,6 +316,25 @@ def run_promote(dev, steps=100, warmup=10):
         out[mode] = {"p50_us": round(statistics.median(lat), 1),
                      "p90_us": round(lat[int(0.9 * (len(lat) - 1))], 1), "runs": len(lat)}
         log(f"promote4k {mode}: p50 {out[mode]['p50_us']} us")
+    # swap of the same request into a pinned host page pool and back
+    from paceserve_amd.kv_transfer import ops
+    dpool = ops.PagedPool(src)
+    hpool = ops.HostPagePool.like(dpool, len(w.src_tables[0]))
+    hids = list(range(len(w.src_tables[0])))
+    for name, fn in (("swap_out", lambda: ops.swap_out(dpool, w.src_tables[0], hpool, hids)),
+                     ("swap_in", lambda: ops.swap_in(hpool, hids, ops.PagedPool(dst), w.src_tables[0]))):
+        lat = []
+        for i in range(warmup + max(20, steps // 5)):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            if i >= warmup:
+                lat.append((time.perf_counter() - t0) * 1e6)
+        lat.sort()
+        out[name] = {"p50_us": round(statistics.median(lat), 1),
+                     "gbs": round(w.payload_bytes / (statistics.median(lat) * 1e-6) / 1e9, 2), "runs": len(lat)}
+        log(f"promote4k {name}: p50 {out[name]['p50_us']} us ({out[name]['gbs']} GB/s)")
     out["payload_bytes"] = w.payload_bytes
     return out
 

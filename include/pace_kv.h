@@ -110,6 +110,34 @@ int pace_kv_move(const void* const* src_layers, int64_t src_pool_pages,
                  int num_layers, int64_t n_pages, int64_t page_bytes,
                  int32_t* err_count, void* stream);
 
+/*
+ * SWAP OUT / SWAP IN between a device pool and a host-resident pool of pages
+ * in pinned memory (hipHostMalloc / torch pin_memory), in one kernel that
+ * reads or writes the host pages across PCIe directly (no staging buffer):
+ *   swap_out: host_layers[l][host_ids[j]] = dev_layers[l][dev_ids[j]]
+ *   swap_in:  dev_layers[l][dev_ids[j]]   = host_layers[l][host_ids[j]]
+ * Host layers have the device pool's layout [host_pool_pages, 2, P, H, D].
+ * Every layer pointer is checked on the host before launch: host layers must
+ * be pinned host memory mapped for the device and device layers memory of the
+ * current device, each allocation holding pool_pages * page_bytes from the
+ * pointer (else PACE_KV_EINVAL / PACE_KV_ERANGE).  Page ids are device int32.
+ *
+ * Replaces the preemption swap of a decode instance: get_kv_cache without
+ * free into host DRAM and the later re-insertion
+ * (paceserve/engine/decode_llm_engine.py:31-41,
+ *  paceserve/disutil/decode_instance.py:176-192).
+ */
+int pace_kv_swap_out(const void* const* dev_layers, int64_t dev_pool_pages,
+                     const int32_t* dev_ids, void* const* host_layers,
+                     int64_t host_pool_pages, const int32_t* host_ids,
+                     int num_layers, int64_t n_pages, int64_t page_bytes,
+                     int32_t* err_count, void* stream);
+int pace_kv_swap_in(const void* const* host_layers, int64_t host_pool_pages,
+                    const int32_t* host_ids, void* const* dev_layers,
+                    int64_t dev_pool_pages, const int32_t* dev_ids,
+                    int num_layers, int64_t n_pages, int64_t page_bytes,
+                    int32_t* err_count, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Pinned-host staging (the host leg of a migration)                         */
 /* ------------------------------------------------------------------------ */

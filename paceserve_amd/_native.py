@@ -34,6 +34,8 @@ SIGNATURES = {
     "pace_kv_pack": (c_int, [_VP, c_int, c_int64, _VP, c_int64, c_int64, _VP, c_int64, _VP, _VP]),
     "pace_kv_unpack": (c_int, [_VP, c_int64, _VP, c_int, c_int64, _VP, c_int64, c_int64, _VP, _VP]),
     "pace_kv_move": (c_int, [_VP, c_int64, _VP, _VP, c_int64, _VP, c_int, c_int64, c_int64, _VP, _VP]),
+    "pace_kv_swap_out": (c_int, [_VP, c_int64, _VP, _VP, c_int64, _VP, c_int, c_int64, c_int64, _VP, _VP]),
+    "pace_kv_swap_in": (c_int, [_VP, c_int64, _VP, _VP, c_int64, _VP, c_int, c_int64, c_int64, _VP, _VP]),
     "pace_kv_stager_create": (c_int, [c_int64, c_int, POINTER(c_void_p)]),
     "pace_kv_stager_destroy": (c_int, [_VP]),
     "pace_kv_pack_to_host": (

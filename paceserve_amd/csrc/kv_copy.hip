@@ -185,6 +185,71 @@ int launch_page_copy(const Side& src, const Side& dst, int num_layers, int64_t n
   return PACE_KV_OK;
 }
 
+// Resolves num_layers host or device layer pointers to the addresses the
+// kernel uses, after checking that each lies in a registered allocation of
+// the expected kind (pinned host memory mapped for the device, or device
+// memory of the current device) that holds pool_bytes from the pointer on.
+// Unregistered (pageable) host memory is rejected: the kernel would fault.
+int resolve_layers(const void* const* layers, int num_layers, int64_t pool_bytes, bool host,
+                   std::vector<const char*>& out, const char* what) {
+  if (num_layers > 0 && layers == nullptr) return fail(PACE_KV_EINVAL, "%s: layer table is NULL", what);
+  int dev = -1;
+  PACE_KV_TRY(hip_status(hipGetDevice(&dev), "hipGetDevice"));
+  out.resize(num_layers);
+  for (int l = 0; l < num_layers; ++l) {
+    const void* p = layers[l];
+    hipPointerAttribute_t attr;
+    memset(&attr, 0, sizeof(attr));
+    hipError_t e = hipPointerGetAttributes(&attr, p);
+    const hipMemoryType want = host ? hipMemoryTypeHost : hipMemoryTypeDevice;
+    if (e != hipSuccess || attr.type != want || attr.devicePointer == nullptr) {
+      (void)hipGetLastError();
+      return fail(PACE_KV_EINVAL, "%s: layer %d is not %s memory", what, l,
+                  host ? "pinned host (hipHostMalloc)" : "device");
+    }
+    if (!host && attr.device != dev)
+      return fail(PACE_KV_EINVAL, "%s: layer %d lives on device %d, current device is %d", what, l,
+                  attr.device, dev);
+    hipDeviceptr_t start = nullptr;
+    size_t size = 0;
+    e = hipPointerGetAttribute(&start, HIP_POINTER_ATTRIBUTE_RANGE_START_ADDR, const_cast<void*>(p));
+    if (e == hipSuccess)
+      e = hipPointerGetAttribute(&size, HIP_POINTER_ATTRIBUTE_RANGE_SIZE, const_cast<void*>(p));
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(PACE_KV_EINVAL, "%s: layer %d allocation range unknown", what, l);
+    }
+    const uintptr_t begin = reinterpret_cast<uintptr_t>(p);
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(start);
+    if (begin < lo || begin - lo + static_cast<uint64_t>(pool_bytes) > size)
+      return fail(PACE_KV_ERANGE, "%s: layer %d allocation holds %zu bytes from its start, "
+                  "the pool needs %lld from offset %llu", what, l, size, (long long)pool_bytes,
+                  (unsigned long long)(begin - lo));
+    out[l] = static_cast<const char*>(attr.devicePointer);
+  }
+  return PACE_KV_OK;
+}
+
+int swap_copy(const void* const* src_layers, int64_t src_pool_pages, const int32_t* src_ids,
+              bool src_host, const void* const* dst_layers, int64_t dst_pool_pages,
+              const int32_t* dst_ids, bool dst_host, int num_layers, int64_t n_pages,
+              int64_t page_bytes, int32_t* err_count, hipStream_t stream, const char* what) {
+  if (num_layers < 0 || n_pages < 0) return fail(PACE_KV_EINVAL, "%s: negative size", what);
+  if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
+  if (src_ids == nullptr || dst_ids == nullptr) return fail(PACE_KV_EINVAL, "%s: NULL page ids", what);
+  if (page_bytes <= 0 || page_bytes % kVecBytes != 0)
+    return fail(PACE_KV_EINVAL, "%s: page_bytes must be a positive multiple of 16", what);
+  if (src_pool_pages < 0 || dst_pool_pages < 0 || src_pool_pages > INT64_MAX / page_bytes ||
+      dst_pool_pages > INT64_MAX / page_bytes)
+    return fail(PACE_KV_EINVAL, "%s: bad pool size", what);
+  std::vector<const char*> s, d;
+  PACE_KV_TRY(resolve_layers(src_layers, num_layers, src_pool_pages * page_bytes, src_host, s, what));
+  PACE_KV_TRY(resolve_layers(dst_layers, num_layers, dst_pool_pages * page_bytes, dst_host, d, what));
+  Side src{s.data(), src_ids, src_pool_pages};
+  Side dst{d.data(), dst_ids, dst_pool_pages};
+  return launch_page_copy(src, dst, num_layers, n_pages, page_bytes, err_count, stream);
+}
+
 }  // namespace pace_kv
 
 using pace_kv::fail;
@@ -230,6 +295,26 @@ int pace_kv_unpack(const void* buf, int64_t buf_layer_stride, void* const* dst_l
   Side dst{reinterpret_cast<const char* const*>(dst_layers), page_ids, pool_pages};
   return pace_kv::launch_page_copy(src, dst, num_layers, n_pages, page_bytes, err_count,
                                    static_cast<hipStream_t>(stream));
+}
+
+int pace_kv_swap_out(const void* const* dev_layers, int64_t dev_pool_pages, const int32_t* dev_ids,
+                     void* const* host_layers, int64_t host_pool_pages, const int32_t* host_ids,
+                     int num_layers, int64_t n_pages, int64_t page_bytes, int32_t* err_count,
+                     void* stream) {
+  return pace_kv::swap_copy(dev_layers, dev_pool_pages, dev_ids, false,
+                            reinterpret_cast<const void* const*>(host_layers), host_pool_pages,
+                            host_ids, true, num_layers, n_pages, page_bytes, err_count,
+                            static_cast<hipStream_t>(stream), "swap_out");
+}
+
+int pace_kv_swap_in(const void* const* host_layers, int64_t host_pool_pages, const int32_t* host_ids,
+                    void* const* dev_layers, int64_t dev_pool_pages, const int32_t* dev_ids,
+                    int num_layers, int64_t n_pages, int64_t page_bytes, int32_t* err_count,
+                    void* stream) {
+  return pace_kv::swap_copy(host_layers, host_pool_pages, host_ids, true,
+                            reinterpret_cast<const void* const*>(dev_layers), dev_pool_pages,
+                            dev_ids, false, num_layers, n_pages, page_bytes, err_count,
+                            static_cast<hipStream_t>(stream), "swap_in");
 }
 
 int pace_kv_move(const void* const* src_layers, int64_t src_pool_pages, const int32_t* src_ids,

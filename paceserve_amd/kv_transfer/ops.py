@@ -31,9 +31,10 @@ def _stream_handle(device: torch.device) -> int:
 
 
 class PagedPool:
-    """Per-layer paged KV tensors of one cache, plus their cached layer table."""
+    """Per-layer paged KV tensors of one cache, plus their cached layer table.
+    host=True builds a host-resident pool of pinned tensors (see HostPagePool)."""
 
-    def __init__(self, layers: Sequence[torch.Tensor]):
+    def __init__(self, layers: Sequence[torch.Tensor], host: bool = False):
         layers = list(layers)
         if not layers:
             raise ValueError("a pool needs at least one layer tensor")
@@ -46,8 +47,12 @@ class PagedPool:
                 raise ValueError(f"layer {i} differs in shape/dtype/device from layer 0")
             if not t.is_contiguous():
                 raise ValueError(f"layer {i} is not contiguous")
-        if first.device.type != "cuda":
+        if host:
+            if first.device.type != "cpu" or not all(t.is_pinned() for t in layers):
+                raise ValueError("host pool layers must be pinned CPU tensors")
+        elif first.device.type != "cuda":
             raise ValueError("pool layers must be device tensors")
+        self.host = host
         self.layers: List[torch.Tensor] = layers
         self.num_layers = len(layers)
         self.num_pages = int(first.shape[0])
@@ -77,6 +82,20 @@ class PagedPool:
         if not (0 <= layer_begin <= end <= self.num_layers):
             raise ValueError(f"layer range [{layer_begin}, {end}) outside [0, {self.num_layers})")
         return layer_begin, end
+
+
+class HostPagePool(PagedPool):
+    """A host-resident pool of pages in pinned memory with the device pool's
+    layout: where a preempted request's pages wait until they are swapped back."""
+
+    def __init__(self, num_layers: int, num_pages: int, page_shape: Tuple[int, ...], dtype: torch.dtype):
+        layers = [torch.empty((num_pages,) + tuple(page_shape), dtype=dtype, pin_memory=True)
+                  for _ in range(num_layers)]
+        super().__init__(layers, host=True)
+
+    @classmethod
+    def like(cls, pool: PagedPool, num_pages: int) -> "HostPagePool":
+        return cls(pool.num_layers, num_pages, pool.page_shape, pool.dtype)
 
 
 def as_pool(pool_or_layers) -> PagedPool:
@@ -178,6 +197,46 @@ def move(src, src_ids: IdsLike, dst, dst_ids: IdsLike, *, layer_begin: int = 0,
     _native.check(_native.load().pace_kv_move(
         sp.table(lb), sp.num_pages, s_ids.data_ptr(), dp.table(lb), dp.num_pages,
         d_ids.data_ptr(), le - lb, n, sp.page_bytes, _err_ptr(err), _stream_handle(sp.device)))
+
+
+def _swap_args(dev: PagedPool, host: PagedPool, dev_ids: IdsLike, host_ids: IdsLike):
+    if not host.host or dev.host:
+        raise ValueError("swap needs one device pool and one host pool")
+    if dev.page_shape != host.page_shape or dev.dtype != host.dtype or dev.num_layers != host.num_layers:
+        raise ValueError("device and host pools differ in layout, layers or dtype")
+    d_ids = device_ids(dev_ids, dev.device)
+    h_ids = device_ids(host_ids, dev.device)
+    if d_ids.numel() != h_ids.numel():
+        raise ValueError(f"{d_ids.numel()} device ids but {h_ids.numel()} host ids")
+    return d_ids, h_ids
+
+
+def swap_out(dev_pool, dev_ids: IdsLike, host_pool: PagedPool, host_ids: IdsLike, *,
+             err: Optional[torch.Tensor] = None) -> None:
+    """host_pool.layers[l][host_ids[j]] = dev_pool.layers[l][dev_ids[j]], one
+    kernel writing the pinned host pages across PCIe."""
+    dev = as_pool(dev_pool)
+    d_ids, h_ids = _swap_args(dev, host_pool, dev_ids, host_ids)
+    n = d_ids.numel()
+    if n == 0:
+        return
+    _native.check(_native.load().pace_kv_swap_out(
+        dev.table(), dev.num_pages, d_ids.data_ptr(), host_pool.table(), host_pool.num_pages,
+        h_ids.data_ptr(), dev.num_layers, n, dev.page_bytes, _err_ptr(err), _stream_handle(dev.device)))
+
+
+def swap_in(host_pool: PagedPool, host_ids: IdsLike, dev_pool, dev_ids: IdsLike, *,
+            err: Optional[torch.Tensor] = None) -> None:
+    """dev_pool.layers[l][dev_ids[j]] = host_pool.layers[l][host_ids[j]], one
+    kernel reading the pinned host pages across PCIe."""
+    dev = as_pool(dev_pool)
+    d_ids, h_ids = _swap_args(dev, host_pool, dev_ids, host_ids)
+    n = d_ids.numel()
+    if n == 0:
+        return
+    _native.check(_native.load().pace_kv_swap_in(
+        host_pool.table(), host_pool.num_pages, h_ids.data_ptr(), dev.table(), dev.num_pages,
+        d_ids.data_ptr(), dev.num_layers, n, dev.page_bytes, _err_ptr(err), _stream_handle(dev.device)))
 
 
 class Promoter:

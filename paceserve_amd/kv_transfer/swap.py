@@ -1,0 +1,62 @@
+"""Swap space for preempted requests: a host-resident pinned page pool.
+
+The reference parks a preempted decode request's KV cache in host DRAM by
+packing it into a KVobj without freeing the worker's pages, and re-inserts it
+when the request is scheduled again (paceserve/engine/decode_llm_engine.py:31-41,
+paceserve/worker/base_worker.py:245-247, paceserve/disutil/decode_instance.py:176-192).
+SwapSpace keeps those pages in a paged host pool instead: swap_out moves a
+request's device pages into host pages allocated from the host pool's own LIFO
+allocator (one kernel writing pinned memory across PCIe) and swap_in moves them
+back into newly allocated device pages, after which the host pages are free.
+"""
+from __future__ import annotations
+
+from typing import Dict, List, Optional
+
+import torch
+
+from ..core.block_manager import NativeBlockAllocator
+from . import ops
+from .kv_utils import normalize_page_ids
+
+
+class SwapSpace:
+    def __init__(self, dev_pool, num_host_pages: int):
+        self.dev = ops.as_pool(dev_pool)
+        self.host = ops.HostPagePool.like(self.dev, num_host_pages)
+        self.host_allocator = NativeBlockAllocator(self.dev.page_shape[1], num_host_pages)
+        self.tables: Dict[str, List[int]] = {}   # seq_id -> host pages
+
+    def num_free_host_pages(self) -> int:
+        return self.host_allocator.get_num_free_blocks()
+
+    def swap_out(self, seq_id: str, dev_table: List[int]) -> List[int]:
+        """Copies the request's device pages into newly allocated host pages;
+        the device pages stay allocated (the caller frees them)."""
+        if seq_id in self.tables:
+            raise ValueError(f"sequence {seq_id} is already swapped out")
+        ids = normalize_page_ids(dev_table, self.dev.num_pages)
+        host_table = self.host_allocator.allocate_many(len(ids))
+        try:
+            ops.swap_out(self.dev, ids, self.host, host_table)
+        except Exception:
+            self.host_allocator.free_many(reversed(host_table))
+            raise
+        self.tables[seq_id] = host_table
+        return host_table
+
+    def swap_in(self, seq_id: str, dev_table: List[int]) -> None:
+        """Copies the request's host pages into dev_table (allocated by the
+        caller) and returns the host pages to the host allocator.  The copy is
+        ordered before later work on the current stream, which is where a
+        reuse of those host pages would be enqueued."""
+        host_table = self.tables.pop(seq_id)
+        ids = normalize_page_ids(dev_table, self.dev.num_pages)
+        if len(ids) != len(host_table):
+            self.tables[seq_id] = host_table
+            raise ValueError(f"{len(ids)} device pages for {len(host_table)} swapped pages")
+        ops.swap_in(self.host, host_table, self.dev, ids)
+        self.host_allocator.free_many(host_table)
+
+    def holds(self, seq_id: str) -> bool:
+        return seq_id in self.tables

