@@ -211,6 +211,48 @@ int pace_kv_roundtrip(pace_kv_stager* stager,
                       int32_t* err_count, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Paged append (the producer of page contents)                              */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Writes the K and V rows of nnz appended tokens into one layer's paged cache
+ * [num_pages, 2, page_size, H, D]:
+ *   b = batch_indices[i], pos = positions[i],
+ *   page = kv_indices[kv_indptr[b] + pos / page_size], slot = pos % page_size,
+ *   cache[page][0][slot] = keys[i], cache[page][1][slot] = values[i]
+ * keys / values hold nnz rows of row_bytes = H * D * elem bytes, token_stride
+ * bytes apart (device).  batch_indices, positions (nnz), kv_indptr
+ * (batch_size + 1) and kv_indices (num_indices) are device int32 arrays.
+ * A token whose request, page slot (outside its request's pages) or page id
+ * is out of range is skipped and counted in err_count.
+ *
+ * Replaces flashinfer.append_paged_kv_cache as called in
+ * paceserve/model_executor/attention/flashinfer_attention_wrapper.py:245-255.
+ */
+int pace_kv_append(const void* keys, const void* values, int64_t token_stride_bytes,
+                   int64_t nnz, const int32_t* batch_indices, const int32_t* positions,
+                   int batch_size, void* cache, int64_t num_pages,
+                   const int32_t* kv_indices, int64_t num_indices,
+                   const int32_t* kv_indptr, int page_size, int64_t row_bytes,
+                   int32_t* err_count, void* stream);
+
+/*
+ * Request index and sequence position of every appended token (device):
+ *   for append_indptr[b] <= i < append_indptr[b+1]:
+ *     batch_indices[i] = b,
+ *     positions[i] = seq_lens[b] - (append_indptr[b+1] - append_indptr[b]) + (i - append_indptr[b])
+ * where seq_lens[b] counts the request's tokens including the appended ones
+ * (max(pages - 1, 0) * page_size + last_page_len).  Tokens beyond
+ * append_indptr[batch_size] get -1, which the append skips.
+ *
+ * Replaces flashinfer.get_batch_indices_positions as called in
+ * paceserve/model_executor/attention/flashinfer_attention_wrapper.py:242.
+ */
+int pace_kv_batch_indices_positions(const int32_t* append_indptr, const int32_t* seq_lens,
+                                    int batch_size, int64_t nnz, int32_t* batch_indices,
+                                    int32_t* positions, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Native block allocation, batch planning and single-call promotion          */
 /* ------------------------------------------------------------------------ */
 

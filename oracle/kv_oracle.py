@@ -20,6 +20,11 @@ tests/test_oracle.py):
     returns the freed pages; exhaustion raises the reference's message.
   - remap_dst_table: the three cases of the rule (len n, n+1, anything else).
   - pages_for_tokens / last_page_len: brute-force slot filling.
+  - get_seq_lens / get_batch_indices_positions / append_paged_kv_cache: the
+    reference's FlashInfer example as a known answer (fixture
+    tests/golden/layout_flashinfer_example.npz, written by a token loop in
+    make_golden.py), and consistency: appending a sequence token by token
+    (decode steps) equals appending it at once (prefill), in any chunking.
 """
 from __future__ import annotations
 
@@ -184,3 +189,51 @@ def torch_cpu_pack_unpack(src_layers, src_idx, dst_layers, dst_idx, buf=None):
         torch.index_select(s, 0, src_idx, out=buf[i])
         d.index_copy_(0, dst_idx, buf[i])
     return buf
+
+
+# --------------------------------------------------------------------------
+# Paged append (the producer of page contents)
+# --------------------------------------------------------------------------
+# The reference calls FlashInfer (flashinfer==0.2.0, requirements.txt:40; not
+# vendored) at paceserve/model_executor/attention/flashinfer_attention_wrapper.py:
+# 241-255.  Its published semantics are restated here; the known answer is the
+# reference's own example, examples/flashinfer_example.py:76-114.
+
+def get_seq_lens(kv_indptr: Sequence[int], kv_last_page_len: Sequence[int], page_size: int) -> np.ndarray:
+    """Tokens per request: max(pages - 1, 0) * page_size + last_page_len."""
+    ip = np.asarray(kv_indptr, dtype=np.int64)
+    pages = ip[1:] - ip[:-1]
+    return np.maximum(pages - 1, 0) * page_size + np.asarray(kv_last_page_len, dtype=np.int64)
+
+
+def get_batch_indices_positions(append_indptr: Sequence[int], seq_lens: Sequence[int], nnz: int):
+    """(batch_indices, positions): appended token t of request b is the
+    request's token seq_lens[b] - append_len[b] + t."""
+    bi = np.full(nnz, -1, dtype=np.int64)
+    pos = np.full(nnz, -1, dtype=np.int64)
+    for b in range(len(append_indptr) - 1):
+        a0, a1 = int(append_indptr[b]), int(append_indptr[b + 1])
+        for t in range(a1 - a0):
+            if a0 + t < nnz:
+                bi[a0 + t] = b
+                pos[a0 + t] = int(seq_lens[b]) - (a1 - a0) + t
+    return bi, pos
+
+
+def append_paged_kv_cache(key: np.ndarray, value: np.ndarray, batch_indices, positions, cache: np.ndarray,
+                          kv_indices, kv_indptr, page_size: int) -> np.ndarray:
+    """Returns a copy of one layer's cache [pages, 2, P, H, D] with token i's K
+    and V rows written to page kv_indices[kv_indptr[b] + pos // P], slot
+    pos % P (K at index 0, V at index 1)."""
+    out = cache.copy()
+    for i in range(key.shape[0]):
+        b, p = int(batch_indices[i]), int(positions[i])
+        if b < 0 or p < 0:
+            continue
+        it = int(kv_indptr[b]) + p // page_size
+        if it >= int(kv_indptr[b + 1]):
+            continue
+        page = int(kv_indices[it])
+        out[page, 0, p % page_size] = key[i]
+        out[page, 1, p % page_size] = value[i]
+    return out

@@ -1,0 +1,123 @@
+"""Paged append on the HIP path (pace_kv_append, pace_kv_batch_indices_positions)
+against the reference's FlashInfer example and the oracle, and the producer ->
+migration -> producer sequence a partially prefilled promotion needs."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as orc
+from paceserve_amd.kv_transfer import append as ap
+from paceserve_amd.kv_transfer import ops
+
+pytestmark = pytest.mark.gpu
+
+WORD = {torch.float16: torch.int16, torch.bfloat16: torch.int16, torch.float32: torch.int32,
+        torch.float8_e4m3fn: torch.uint8}
+
+
+def words(t):
+    return t.view(WORD[t.dtype])
+
+
+def i32(x, dev):
+    return torch.tensor(x, dtype=torch.int32, device=dev)
+
+
+def test_flashinfer_example_known_answer(gpu):
+    with np.load("tests/golden/layout_flashinfer_example.npz", allow_pickle=False) as z:
+        k, v, want = z["k"], z["v"], z["cache"]
+    kk = torch.from_numpy(k.astype(np.int16)).to(gpu).view(torch.float16)
+    vv = torch.from_numpy(v.astype(np.int16)).to(gpu).view(torch.float16)
+    cache = torch.zeros(3, 2, 4, 1, 128, dtype=torch.float16, device=gpu)
+    kv_indptr, kv_indices, last = i32([0, 1, 3], gpu), i32([0, 1, 2], gpu), i32([3, 3], gpu)
+    seq = ap.get_seq_lens(kv_indptr, last, 4)
+    bi, pos = ap.get_batch_indices_positions(i32([0, 3, 10], gpu), seq, 10)
+    assert seq.tolist() == [3, 7] and bi.tolist() == [0] * 3 + [1] * 7
+    assert pos.tolist() == [0, 1, 2, 0, 1, 2, 3, 4, 5, 6]
+    ap.append_paged_kv_cache(kk, vv, bi, pos, cache, kv_indices, kv_indptr, last)
+    torch.cuda.synchronize()
+    assert np.array_equal(words(cache).cpu().numpy().astype(np.uint16), want)
+
+
+@pytest.mark.parametrize("dtype,H,D,P", [
+    (torch.bfloat16, 8, 128, 16), (torch.float16, 32, 128, 16), (torch.float16, 1, 64, 4),
+    (torch.float32, 4, 64, 16), (torch.float8_e4m3fn, 8, 128, 16), (torch.bfloat16, 2, 8, 16)])
+def test_mixed_prefill_and_decode_batch_matches_oracle(gpu, dtype, H, D, P):
+    rng = np.random.default_rng(H * D + P)
+    R = 6
+    prior = rng.integers(0, 40, R)                 # tokens already in each request
+    app = rng.integers(1, 25, R)                   # tokens appended now
+    app[::2] = 1                                   # decode requests append one token
+    total = prior + app
+    pages = -(-total // P)
+    NP = int(pages.sum()) + 5
+    perm = rng.permutation(NP)
+    kv_indptr = np.concatenate([[0], np.cumsum(pages)])
+    kv_indices = perm[: kv_indptr[-1]]
+    last = np.where(total % P == 0, P, total % P)
+    append_indptr = np.concatenate([[0], np.cumsum(app)])
+    nnz = int(append_indptr[-1])
+    wt = WORD[dtype]
+    raw = lambda shape: torch.from_numpy(rng.integers(-2 ** 7, 2 ** 7, shape).astype(np.int8)).to(gpu)
+    k = raw((nnz, H, D * torch.empty(0, dtype=dtype).element_size())).view(dtype).view(nnz, H, D)
+    v = raw((nnz, H, D * torch.empty(0, dtype=dtype).element_size())).view(dtype).view(nnz, H, D)
+    cache = raw((NP, 2, P, H, D * torch.empty(0, dtype=dtype).element_size())).view(dtype).view(NP, 2, P, H, D)
+    want = orc.append_paged_kv_cache(
+        words(k).cpu().numpy(), words(v).cpu().numpy(),
+        *orc.get_batch_indices_positions(append_indptr, orc.get_seq_lens(kv_indptr, last, P), nnz),
+        words(cache).cpu().numpy(), kv_indices, kv_indptr, P)
+    seq = ap.get_seq_lens(i32(kv_indptr, gpu), i32(last, gpu), P)
+    bi, pos = ap.get_batch_indices_positions(i32(append_indptr, gpu), seq, nnz)
+    ap.append_paged_kv_cache(k, v, bi, pos, cache, i32(kv_indices, gpu), i32(kv_indptr, gpu), i32(last, gpu))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(words(cache).cpu().numpy(), want)
+
+
+def test_out_of_range_tokens_are_skipped_and_counted(gpu):
+    cache = torch.zeros(4, 2, 4, 1, 64, dtype=torch.float16, device=gpu)
+    k = torch.ones(4, 1, 64, dtype=torch.float16, device=gpu)
+    kv_indptr, kv_indices = i32([0, 1, 2], gpu), i32([3, 7], gpu)     # page 7 does not exist
+    bi = i32([0, 1, 5, 0], gpu)          # request 5 does not exist
+    pos = i32([1, 0, 0, 4], gpu)         # position 4 is past request 0's single page
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ap.append_paged_kv_cache(k, k, bi, pos, cache, kv_indices, kv_indptr, i32([2, 1], gpu), err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 3
+    assert (cache[3, :, 1] == 1).all() and int((cache != 0).sum()) == 2 * 64
+
+
+def test_partially_prefilled_request_promoted_then_continued(gpu):
+    """Chunk 1 of a prompt is appended into the low-priority pool, the request
+    is promoted (pages moved to the high-priority pool), chunk 2 is appended
+    there: the result equals appending the whole prompt on the high-priority
+    pool directly."""
+    L, H, D, P, NP = 3, 8, 128, 16, 64
+    rng = np.random.default_rng(9)
+    n1, n2 = 37, 50
+    k = torch.randn(L, n1 + n2, H, D, device=gpu).to(torch.bfloat16)
+    v = torch.randn(L, n1 + n2, H, D, device=gpu).to(torch.bfloat16)
+    lp = [torch.zeros(NP, 2, P, H, D, dtype=torch.bfloat16, device=gpu) for _ in range(L)]
+    hp = [torch.zeros(NP, 2, P, H, D, dtype=torch.bfloat16, device=gpu) for _ in range(L)]
+    ref = [torch.zeros(NP, 2, P, H, D, dtype=torch.bfloat16, device=gpu) for _ in range(L)]
+
+    def append(pool, l, table, done, k_new, v_new):
+        total = done + k_new.shape[0]
+        pages = -(-total // P)
+        ip = i32([0, pages], gpu)
+        last = i32([total % P or P], gpu)
+        seq = ap.get_seq_lens(ip, last, P)
+        bi, pos = ap.get_batch_indices_positions(i32([0, k_new.shape[0]], gpu), seq, k_new.shape[0])
+        ap.append_paged_kv_cache(k_new, v_new, bi, pos, pool[l], i32(table[:pages], gpu), ip, last)
+
+    lp_table = rng.permutation(NP)[:6].tolist()         # room for 87 tokens
+    for l in range(L):
+        append(lp, l, lp_table, 0, k[l, :n1], v[l, :n1])
+    n_lp = -(-n1 // P)
+    hp_table = rng.permutation(NP)[:6].tolist()
+    ops.move(lp, lp_table[:n_lp], hp, hp_table[:n_lp])   # promotion of the prefilled pages
+    for l in range(L):
+        append(hp, l, hp_table, n1, k[l, n1:], v[l, n1:])
+        append(ref, l, hp_table, 0, k[l], v[l])
+    torch.cuda.synchronize()
+    for l in range(L):
+        assert torch.equal(words(hp[l]), words(ref[l])), f"layer {l}"

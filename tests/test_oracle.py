@@ -234,3 +234,46 @@ def test_planted_unpack_mistakes_fail_the_fixtures():
     c2 = load("fp16_partial")
     got2 = orc.unpack(c2["packed"], list(c2["dst_before"]), c2["src_table"].tolist())
     assert not np.array_equal(np.stack(got2), c2["dst_after"])
+
+
+# ------------------------------------------------------------ paged append
+
+
+def flashinfer_example():
+    with np.load(GOLDEN / "layout_flashinfer_example.npz", allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def test_append_oracle_reproduces_flashinfer_example():
+    """examples/flashinfer_example.py:76-114: lengths [3, 7], page_size 4,
+    page indptr [0, 1, 3], indices [0, 1, 2], last page lengths [3, 3]."""
+    z = flashinfer_example()
+    kv_indptr, kv_indices, last = [0, 1, 3], [0, 1, 2], [3, 3]
+    seq = orc.get_seq_lens(kv_indptr, last, 4)
+    assert seq.tolist() == [3, 7]
+    bi, pos = orc.get_batch_indices_positions([0, 3, 10], seq, 10)
+    assert bi.tolist() == [0] * 3 + [1] * 7
+    assert pos.tolist() == [0, 1, 2, 0, 1, 2, 3, 4, 5, 6]
+    cache = np.zeros((3, 2, 4, 1, 128), dtype=np.uint16)
+    got = orc.append_paged_kv_cache(z["k"], z["v"], bi, pos, cache, kv_indices, kv_indptr, 4)
+    np.testing.assert_array_equal(got, z["cache"])
+
+
+@pytest.mark.parametrize("chunks", [[10], [1] * 10, [4, 3, 3], [7, 1, 1, 1]])
+def test_append_in_chunks_equals_append_at_once(chunks):
+    rng = np.random.default_rng(sum(chunks) * len(chunks))
+    P, pages = 4, [5, 2, 7]
+    k = rng.integers(0, 2 ** 16, (10, 2, 8), dtype=np.uint16)
+    v = rng.integers(0, 2 ** 16, (10, 2, 8), dtype=np.uint16)
+    cache0 = rng.integers(0, 2 ** 16, (8, 2, P, 2, 8), dtype=np.uint16)
+    once_bi, once_pos = orc.get_batch_indices_positions([0, 10], [10], 10)
+    once = orc.append_paged_kv_cache(k, v, once_bi, once_pos, cache0, pages, [0, 3], P)
+    cache, done = cache0, 0
+    for c in chunks:                      # the sequence grows chunk by chunk
+        total = done + c
+        n_pages = -(-total // P)
+        seq = orc.get_seq_lens([0, n_pages], [total % P or P], P)
+        bi, pos = orc.get_batch_indices_positions([0, c], seq, c)
+        cache = orc.append_paged_kv_cache(k[done:total], v[done:total], bi, pos, cache, pages, [0, n_pages], P)
+        done = total
+    np.testing.assert_array_equal(cache, once)
