@@ -32,12 +32,18 @@ struct Side {
   int64_t pool_pages;         // ids must lie in [0, pool_pages)
 };
 
+// Most page ids per side that a launch carries in its kernel arguments.
+#define PACE_KV_INLINE_IDS 512
+
 // Validates arguments and enqueues the copy dst[l][dst_id(j)] = src[l][src_id(j)]
 // for l < num_layers, j < n_pages on `stream`, in launches of at most
-// PACE_KV_MAX_LAYERS_PER_LAUNCH layers.
+// PACE_KV_MAX_LAYERS_PER_LAUNCH layers.  host_src_ids / host_dst_ids (host
+// arrays, n_pages <= PACE_KV_INLINE_IDS) replace the sides' device ids and
+// travel in the kernel arguments.
 int launch_page_copy(const Side& src, const Side& dst, int num_layers,
                      int64_t n_pages, int64_t page_bytes, int32_t* err_count,
-                     hipStream_t stream);
+                     hipStream_t stream, const int32_t* host_src_ids = nullptr,
+                     const int32_t* host_dst_ids = nullptr);
 
 // Builds the layer table of a contiguous buffer [num_layers][layer_stride].
 void buffer_layers(const void* base, int64_t layer_stride, int num_layers,

@@ -59,18 +59,28 @@ struct CopyParams {
   uint32_t page_vecs;      // page_bytes / 16
 };
 
-// GUARD: page_bytes is not a multiple of kRowBytes, so the last row of a page
-// is partial.
+// Page ids carried in the kernel arguments (small promotions): no device id
+// array, so no upload has to precede the launch.
+struct CopyParamsInline {
+  CopyParams base;
+  int32_t src_ids[PACE_KV_INLINE_IDS];
+  int32_t dst_ids[PACE_KV_INLINE_IDS];
+};
+
+__device__ __forceinline__ uint32_t page_of(const int32_t* ids, uint32_t j) {
+  return ids ? static_cast<uint32_t>(ids[j]) : j;
+}
+
+// The copy of one 1 KiB row; shared by both id sources.
 template <bool GUARD>
-__global__ __launch_bounds__(kThreads) void page_copy_kernel(const CopyParams p) {
-  const uint32_t item = blockIdx.x;
-  if (item >= p.total_items) return;
+__device__ __forceinline__ void copy_row(const CopyParams& p, uint32_t item, bool inline_ids,
+                                         const int32_t* isrc, const int32_t* idst) {
   const uint32_t page_linear = item / p.rows_per_page;
   const uint32_t row = item - page_linear * p.rows_per_page;
   const uint32_t layer = page_linear / p.n_pages;
   const uint32_t j = page_linear - layer * p.n_pages;
-  const uint32_t sp = p.src_ids ? static_cast<uint32_t>(p.src_ids[j]) : j;
-  const uint32_t dp = p.dst_ids ? static_cast<uint32_t>(p.dst_ids[j]) : j;
+  const uint32_t sp = inline_ids ? page_of(isrc, j) : page_of(p.src_ids, j);
+  const uint32_t dp = inline_ids ? page_of(idst, j) : page_of(p.dst_ids, j);
   // Negative ids wrap to large unsigned values and fail the same test.
   if (sp >= p.src_pool_pages || dp >= p.dst_pool_pages) {
     if (row == 0 && threadIdx.x == 0 && p.err != nullptr) atomicAdd(p.err, 1);
@@ -85,11 +95,49 @@ __global__ __launch_bounds__(kThreads) void page_copy_kernel(const CopyParams p)
   __builtin_nontemporal_store(__builtin_nontemporal_load(s), d);
 }
 
+// GUARD: page_bytes is not a multiple of kRowBytes, so the last row of a page
+// is partial.
+template <bool GUARD>
+__global__ __launch_bounds__(kThreads) void page_copy_kernel(const CopyParams p) {
+  const uint32_t item = blockIdx.x;
+  if (item >= p.total_items) return;
+  copy_row<GUARD>(p, item, false, nullptr, nullptr);
+}
+
+// Same copy with the ids in the kernel arguments.  A side whose ids are not
+// inline (the contiguous buffer of a pack or unpack) is marked by a null
+// pointer in the base parameters and indexes pages by position.
+template <bool GUARD, bool SRC_INLINE, bool DST_INLINE>
+__global__ __launch_bounds__(kThreads) void page_copy_inline_kernel(const CopyParamsInline p) {
+  const uint32_t item = blockIdx.x;
+  if (item >= p.base.total_items) return;
+  copy_row<GUARD>(p.base, item, true, SRC_INLINE ? p.src_ids : nullptr,
+                  DST_INLINE ? p.dst_ids : nullptr);
+}
+
 template <bool GUARD>
 hipError_t launch(const CopyParams& p, hipStream_t stream) {
   void* args[] = {const_cast<CopyParams*>(&p)};
   return hipLaunchKernel(reinterpret_cast<const void*>(&page_copy_kernel<GUARD>),
                          dim3(p.total_items), dim3(kThreads), args, 0, stream);
+}
+
+template <bool GUARD, bool S, bool D>
+hipError_t launch_inline_t(const CopyParamsInline& p, hipStream_t stream) {
+  void* args[] = {const_cast<CopyParamsInline*>(&p)};
+  return hipLaunchKernel(reinterpret_cast<const void*>(&page_copy_inline_kernel<GUARD, S, D>),
+                         dim3(p.base.total_items), dim3(kThreads), args, 0, stream);
+}
+
+hipError_t launch_inline(const CopyParamsInline& p, bool guard, bool s, bool d, hipStream_t stream) {
+  if (guard) {
+    if (s && d) return launch_inline_t<true, true, true>(p, stream);
+    if (s) return launch_inline_t<true, true, false>(p, stream);
+    return launch_inline_t<true, false, true>(p, stream);
+  }
+  if (s && d) return launch_inline_t<false, true, true>(p, stream);
+  if (s) return launch_inline_t<false, true, false>(p, stream);
+  return launch_inline_t<false, false, true>(p, stream);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -126,7 +174,8 @@ void buffer_layers(const void* base, int64_t layer_stride, int num_layers, const
 }
 
 int launch_page_copy(const Side& src, const Side& dst, int num_layers, int64_t n_pages,
-                     int64_t page_bytes, int32_t* err_count, hipStream_t stream) {
+                     int64_t page_bytes, int32_t* err_count, hipStream_t stream,
+                     const int32_t* host_src_ids, const int32_t* host_dst_ids) {
   if (num_layers < 0) return fail(PACE_KV_EINVAL, "num_layers must be >= 0 (got %d)", num_layers);
   if (n_pages < 0) return fail(PACE_KV_EINVAL, "n_pages must be >= 0 (got %lld)", (long long)n_pages);
   if (page_bytes <= 0 || page_bytes % kVecBytes != 0)
@@ -137,12 +186,18 @@ int launch_page_copy(const Side& src, const Side& dst, int num_layers, int64_t n
   if (n_pages > INT32_MAX) return fail(PACE_KV_ERANGE, "n_pages exceeds int32 range");
   if (src.pool_pages < 0 || dst.pool_pages < 0) return fail(PACE_KV_EINVAL, "pool_pages must be >= 0");
   if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
-  if ((src.ids == nullptr && src.pool_pages < n_pages) || (dst.ids == nullptr && dst.pool_pages < n_pages))
+  const bool src_indexed = src.ids != nullptr || host_src_ids != nullptr;
+  const bool dst_indexed = dst.ids != nullptr || host_dst_ids != nullptr;
+  if ((!src_indexed && src.pool_pages < n_pages) || (!dst_indexed && dst.pool_pages < n_pages))
     return fail(PACE_KV_ERANGE, "contiguous buffer holds fewer pages than n_pages");
   int rc = check_layers(src.layers, num_layers, "source");
   if (rc) return rc;
   rc = check_layers(dst.layers, num_layers, "destination");
   if (rc) return rc;
+  const bool inline_ids = host_src_ids != nullptr || host_dst_ids != nullptr;
+  if (inline_ids && n_pages > PACE_KV_INLINE_IDS)
+    return fail(PACE_KV_ERANGE, "more than %d pages cannot travel in the kernel arguments",
+                PACE_KV_INLINE_IDS);
   if (src.ids != nullptr && (reinterpret_cast<uintptr_t>(src.ids) & 3u))
     return fail(PACE_KV_EINVAL, "source page ids are not 4-byte aligned");
   if (dst.ids != nullptr && (reinterpret_cast<uintptr_t>(dst.ids) & 3u))
@@ -165,20 +220,29 @@ int launch_page_copy(const Side& src, const Side& dst, int num_layers, int64_t n
       CopyParams p;
       memset(&p, 0, sizeof(p));
       for (int l = 0; l < nl; ++l) {
-        p.src[l] = src.layers[l0 + l] + (src.ids ? 0 : j0 * page_bytes);
-        p.dst[l] = const_cast<char*>(dst.layers[l0 + l]) + (dst.ids ? 0 : j0 * page_bytes);
+        p.src[l] = src.layers[l0 + l] + (src_indexed ? 0 : j0 * page_bytes);
+        p.dst[l] = const_cast<char*>(dst.layers[l0 + l]) + (dst_indexed ? 0 : j0 * page_bytes);
       }
       p.src_ids = src.ids ? src.ids + j0 : nullptr;
       p.dst_ids = dst.ids ? dst.ids + j0 : nullptr;
       p.err = err_count;
       p.page_bytes = page_bytes;
-      p.src_pool_pages = src.ids ? clamp_pool(src.pool_pages) : static_cast<uint32_t>(nj);
-      p.dst_pool_pages = dst.ids ? clamp_pool(dst.pool_pages) : static_cast<uint32_t>(nj);
+      p.src_pool_pages = src_indexed ? clamp_pool(src.pool_pages) : static_cast<uint32_t>(nj);
+      p.dst_pool_pages = dst_indexed ? clamp_pool(dst.pool_pages) : static_cast<uint32_t>(nj);
       p.n_pages = static_cast<uint32_t>(nj);
       p.rows_per_page = static_cast<uint32_t>(rows_per_page);
       p.total_items = static_cast<uint32_t>(int64_t(nl) * nj * rows_per_page);
       p.page_vecs = static_cast<uint32_t>(page_bytes / kVecBytes);
-      rc = hip_status(guard ? launch<true>(p, stream) : launch<false>(p, stream), "page copy launch");
+      if (inline_ids) {
+        CopyParamsInline q;
+        q.base = p;
+        if (host_src_ids) memcpy(q.src_ids, host_src_ids + j0, nj * sizeof(int32_t));
+        if (host_dst_ids) memcpy(q.dst_ids, host_dst_ids + j0, nj * sizeof(int32_t));
+        rc = hip_status(launch_inline(q, guard, host_src_ids != nullptr, host_dst_ids != nullptr, stream),
+                        "page copy launch");
+      } else {
+        rc = hip_status(guard ? launch<true>(p, stream) : launch<false>(p, stream), "page copy launch");
+      }
       if (rc) return rc;
     }
   }

@@ -148,6 +148,51 @@ int promoter_reserve(pace_kv_promoter* p, int64_t entries) {
   return PACE_KV_OK;
 }
 
+// Small batches: both id lists travel in the kernel arguments, so no upload
+// (and no slot of the promoter) is involved.
+int promote_inline(pace_kv_promoter* pr, pace_kv_allocator* dst_alloc,
+                   const void* const* src_layers, int64_t src_pool_pages, void* const* dst_layers,
+                   int64_t dst_pool_pages, int num_layers, int64_t page_bytes, int num_requests,
+                   const int64_t* src_indptr, const int32_t* src_ids, const int32_t* dst_pages,
+                   void* buffer, int64_t buffer_layer_stride, int buffer_layers,
+                   int32_t* out_dst_tables, int32_t* err_count, const Plan& plan,
+                   hipStream_t stream) {
+  (void)pr;
+  const int64_t n = plan.n_src;
+  int32_t dst_ids[PACE_KV_INLINE_IDS];
+  PACE_KV_TRY(plan_allocate(dst_alloc, num_requests, src_indptr, dst_pages, plan, out_dst_tables,
+                            dst_ids));
+  using pace_kv::Side;
+  const char* const* src_tab = reinterpret_cast<const char* const*>(src_layers);
+  const char* const* dst_tab = reinterpret_cast<const char* const*>(dst_layers);
+  int rc = PACE_KV_OK;
+  if (n > 0 && num_layers > 0) {
+    if (buffer == nullptr) {
+      rc = pace_kv::launch_page_copy(Side{src_tab, nullptr, src_pool_pages},
+                                     Side{dst_tab, nullptr, dst_pool_pages}, num_layers, n,
+                                     page_bytes, err_count, stream, src_ids, dst_ids);
+    } else {
+      std::vector<const char*> buf(buffer_layers);
+      pace_kv::buffer_layers(buffer, buffer_layer_stride, buffer_layers, buf.data());
+      for (int l0 = 0; l0 < num_layers && rc == PACE_KV_OK; l0 += buffer_layers) {
+        const int nl = num_layers - l0 < buffer_layers ? num_layers - l0 : buffer_layers;
+        rc = pace_kv::launch_page_copy(Side{src_tab + l0, nullptr, src_pool_pages},
+                                       Side{buf.data(), nullptr, n}, nl, n, page_bytes, err_count,
+                                       stream, src_ids, nullptr);
+        if (rc == PACE_KV_OK)
+          rc = pace_kv::launch_page_copy(Side{buf.data(), nullptr, n},
+                                         Side{dst_tab + l0, nullptr, dst_pool_pages}, nl, n,
+                                         page_bytes, err_count, stream, nullptr, dst_ids);
+      }
+    }
+  }
+  if (rc) {
+    std::lock_guard<std::mutex> lock(dst_alloc->mu);
+    unpop_pages(dst_alloc, plan.n_dst_table, out_dst_tables);
+  }
+  return rc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -302,6 +347,12 @@ int pace_kv_promote(pace_kv_promoter* pr, pace_kv_allocator* dst_alloc,
   if (buffer != nullptr && (buffer_layer_stride < n * page_bytes || buffer_layer_stride % 16 != 0))
     return fail(PACE_KV_ERANGE, "promote: buffer_layer_stride must be >= n_pages*page_bytes and a multiple of 16");
   hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (n <= PACE_KV_INLINE_IDS) return promote_inline(pr, dst_alloc, src_layers, src_pool_pages,
+                                                      dst_layers, dst_pool_pages, num_layers,
+                                                      page_bytes, num_requests, src_indptr, src_ids,
+                                                      dst_pages, buffer, buffer_layer_stride,
+                                                      buffer_layers, out_dst_tables, err_count,
+                                                      plan, stream);
 
   PACE_KV_TRY(promoter_reserve(pr, 2 * n));
   const int s = static_cast<int>(pr->calls & 1);
@@ -318,25 +369,23 @@ int pace_kv_promote(pace_kv_promoter* pr, pace_kv_allocator* dst_alloc,
   };
   int32_t* dev_ids = pr->dev[s];
   int rc = hip_status(hipStreamWaitEvent(stream, pr->done[s], 0), "promoter slot wait");
-  if (rc == PACE_KV_OK && n > 0)
+  if (rc == PACE_KV_OK)
     rc = hip_status(hipMemcpyAsync(dev_ids, host, 2 * n * sizeof(int32_t), hipMemcpyHostToDevice, stream),
                     "promoter id upload");
   if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(pr->copied[s], stream), "promoter record");
   if (rc) return rollback(rc);
   ++pr->calls;
-  if (n > 0) {
-    if (buffer == nullptr) {
-      rc = pace_kv_move(src_layers, src_pool_pages, dev_ids, dst_layers, dst_pool_pages, dev_ids + n,
-                        num_layers, n, page_bytes, err_count, stream);
-    } else {
-      for (int l0 = 0; l0 < num_layers && rc == PACE_KV_OK; l0 += buffer_layers) {
-        const int nl = num_layers - l0 < buffer_layers ? num_layers - l0 : buffer_layers;
-        rc = pace_kv_pack(src_layers + l0, nl, src_pool_pages, dev_ids, n, page_bytes, buffer,
-                          buffer_layer_stride, err_count, stream);
-        if (rc == PACE_KV_OK)
-          rc = pace_kv_unpack(buffer, buffer_layer_stride, dst_layers + l0, nl, dst_pool_pages,
-                              dev_ids + n, n, page_bytes, err_count, stream);
-      }
+  if (buffer == nullptr) {
+    rc = pace_kv_move(src_layers, src_pool_pages, dev_ids, dst_layers, dst_pool_pages, dev_ids + n,
+                      num_layers, n, page_bytes, err_count, stream);
+  } else {
+    for (int l0 = 0; l0 < num_layers && rc == PACE_KV_OK; l0 += buffer_layers) {
+      const int nl = num_layers - l0 < buffer_layers ? num_layers - l0 : buffer_layers;
+      rc = pace_kv_pack(src_layers + l0, nl, src_pool_pages, dev_ids, n, page_bytes, buffer,
+                        buffer_layer_stride, err_count, stream);
+      if (rc == PACE_KV_OK)
+        rc = pace_kv_unpack(buffer, buffer_layer_stride, dst_layers + l0, nl, dst_pool_pages,
+                            dev_ids + n, n, page_bytes, err_count, stream);
     }
   }
   // Record even on failure: the slot's next user waits on this event.

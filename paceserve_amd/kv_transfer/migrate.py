@@ -178,21 +178,28 @@ class KVMigrator:
         work is enqueued on the current stream (synchronize to wait).  With a
         NativeBlockAllocator, the device modes run as one library call."""
         if isinstance(self.dst_allocator, NativeBlockAllocator) and mode in ("buffer", "fused"):
+            import itertools
+
             import numpy as np
             counts = [len(t) for t in src_tables]
             indptr = np.zeros(len(counts) + 1, dtype=np.int64)
             np.cumsum(counts, out=indptr[1:])
-            src_flat = [i for t in src_tables for i in normalize_page_ids(t, self.src.num_pages)]
-            src_ids = np.array(src_flat, dtype=np.int32)
-            tables = self.promote_native(src_ids, indptr, dst_pages, mode, layers_per_chunk)
+            flat = np.fromiter(itertools.chain.from_iterable(src_tables), dtype=np.int64,
+                               count=int(indptr[-1]))
+            npages = self.src.num_pages
+            if flat.size and (flat.min() < -npages or flat.max() >= npages):
+                bad = flat[(flat < -npages) | (flat >= npages)][0]
+                raise IndexError(f"index {bad} is out of bounds for dimension 0 with size {npages}")
+            src_ids = np.where(flat < 0, flat + npages, flat).astype(np.int32)
+            tables = self.promote_native(src_ids, indptr, dst_pages, mode, layers_per_chunk).tolist()
             sizes = counts if dst_pages is None else list(dst_pages)
             dst_tables, dst_ids, pos = [], [], 0
             for n, m in zip(counts, sizes):
-                t = tables[pos:pos + m].tolist()
+                t = tables[pos:pos + m]
                 pos += m
                 dst_tables.append(t)
                 dst_ids.extend(t[:n])
-            return MigrationPlan(src_flat, dst_ids, dst_tables, indptr.tolist())
+            return MigrationPlan(src_ids.tolist(), dst_ids, dst_tables, indptr.tolist())
         plan = self.plan(src_tables, dst_pages)
         if plan.n_pages:
             s_ids, d_ids = self.upload(plan)

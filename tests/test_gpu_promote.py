@@ -12,7 +12,7 @@ from paceserve_amd.kv_transfer import migrate, ops
 pytestmark = pytest.mark.gpu
 
 SHAPE = workloads.KVShape(num_layers=6, num_kv_heads=8, head_dim=128, page_size=16, dtype=torch.bfloat16)
-POOL = 256
+POOL = 2048
 
 
 def pools(dev, seed):
@@ -24,11 +24,17 @@ def words(t):
     return t.view(torch.int16)
 
 
+# batches of up to 512 pages carry their ids in the kernel arguments; larger
+# ones go through the promoter's pinned id slots
+SIZES = {"inline": (7, 1, 30, 12), "uploaded": (300, 1, 250, 90)}
+
+
 @pytest.mark.parametrize("mode", ["fused", "buffer"])
-def test_native_promote_matches_python_path(gpu, mode):
+@pytest.mark.parametrize("size", ["inline", "uploaded"])
+def test_native_promote_matches_python_path(gpu, mode, size):
     rng = np.random.default_rng(11)
-    tables = [rng.permutation(POOL)[: int(k)].tolist() for k in (7, 1, 30, 12)]
-    dst_pages = [7, 2, 30, 13]
+    tables = [rng.permutation(POOL)[: int(k)].tolist() for k in SIZES[size]]
+    dst_pages = [len(t) + (i % 2) for i, t in enumerate(tables)]
     free = rng.permutation(POOL).tolist()
     src, dst_py = pools(gpu, 5)
     _, dst_nat = pools(gpu, 5)
@@ -43,7 +49,8 @@ def test_native_promote_matches_python_path(gpu, mode):
         assert torch.equal(words(dst_py.layers[l]), words(dst_nat.layers[l])), f"layer {l}"
 
 
-def test_back_to_back_promotions_reuse_id_slots(gpu):
+@pytest.mark.parametrize("lo,hi", [(1, 20), (513, 700)])
+def test_back_to_back_promotions_reuse_id_slots(gpu, lo, hi):
     """Ten promotions of different sizes without synchronising in between:
     each must land its own pages (a slot overwritten early would scatter
     another call's ids)."""
@@ -53,7 +60,9 @@ def test_back_to_back_promotions_reuse_id_slots(gpu):
     rng = np.random.default_rng(2)
     plans = []
     for i in range(10):
-        n = int(rng.integers(1, 20))
+        if alloc.get_num_free_blocks() < hi:
+            break
+        n = int(rng.integers(lo, hi))
         table = rng.permutation(POOL)[:n].tolist()
         plans.append(mig.promote([table], mode="fused" if i % 2 else "buffer"))
         if i % 3 == 2:                  # return some pages: later calls reuse them
