@@ -40,10 +40,16 @@ struct Side {
 // PACE_KV_MAX_LAYERS_PER_LAUNCH layers.  host_src_ids / host_dst_ids (host
 // arrays, n_pages <= PACE_KV_INLINE_IDS) replace the sides' device ids and
 // travel in the kernel arguments.
+// Store flavour of a copy: kStream always uses nontemporal stores;
+// kTemporalIfSmall (pack) uses plain stores when one launch writes at most
+// 1 GiB, so that the unpack reading the rows next finds them in cache.
+enum class StorePolicy { kStream, kTemporalIfSmall };
+
 int launch_page_copy(const Side& src, const Side& dst, int num_layers,
                      int64_t n_pages, int64_t page_bytes, int32_t* err_count,
                      hipStream_t stream, const int32_t* host_src_ids = nullptr,
-                     const int32_t* host_dst_ids = nullptr);
+                     const int32_t* host_dst_ids = nullptr,
+                     StorePolicy policy = StorePolicy::kStream);
 
 // Builds the layer table of a contiguous buffer [num_layers][layer_stride].
 void buffer_layers(const void* base, int64_t layer_stride, int num_layers,

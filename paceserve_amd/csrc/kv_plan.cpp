@@ -178,7 +178,8 @@ int promote_inline(pace_kv_promoter* pr, pace_kv_allocator* dst_alloc,
         const int nl = num_layers - l0 < buffer_layers ? num_layers - l0 : buffer_layers;
         rc = pace_kv::launch_page_copy(Side{src_tab + l0, nullptr, src_pool_pages},
                                        Side{buf.data(), nullptr, n}, nl, n, page_bytes, err_count,
-                                       stream, src_ids, nullptr);
+                                       stream, src_ids, nullptr,
+                                       pace_kv::StorePolicy::kTemporalIfSmall);
         if (rc == PACE_KV_OK)
           rc = pace_kv::launch_page_copy(Side{buf.data(), nullptr, n},
                                          Side{dst_tab + l0, nullptr, dst_pool_pages}, nl, n,
