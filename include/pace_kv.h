@@ -25,7 +25,9 @@
  *    tile is skipped and, when err_count (a device int32) is non-NULL, counted
  *    there with an atomic add.
  *  - Entry points are reentrant; none holds global locks or synchronises the
- *    device.  A pace_kv_stager must be driven by one host thread at a time.
+ *    device.  A pace_kv_stager or pace_kv_promoter must be driven by one host
+ *    thread at a time; a pace_kv_allocator serialises its callers with its own
+ *    mutex.
  */
 #ifndef PACE_KV_H_
 #define PACE_KV_H_

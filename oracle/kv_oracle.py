@@ -1,8 +1,9 @@
 """CPU oracle of PaceServe's KV-cache migration path.
 
 TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
-CPU-baseline leg may import this module, and only as the checker or the timed
-CPU baseline; the product path (paceserve_amd) never calls it.
+CPU-baseline leg may import this module, and only as the expected answer that
+results are compared with, or as the timed CPU baseline; the product path
+(paceserve_amd) never calls it.
 
 Each function restates one step of the reference's behaviour in plain numpy
 (raw 16-bit words: the path copies bytes, it does no arithmetic) and cites

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/kv_oracle.py) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/kv_oracle.py) before its answers are trusted.
 
 Checks: the committed golden fixtures (written by element-by-element loops in
 tests/golden/make_golden.py), the library routines the reference's indexing
