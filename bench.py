@@ -157,7 +157,7 @@ def run_device(args, w, dev, src, dst, plan, s_ids, d_ids):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "page_copy_kernel<false> (pack and unpack launches)",
+            "kernel": "page_copy_kernel<false, false> (pack and unpack launches, nontemporal stores)",
             "algorithmic_bytes_per_launch": int(statistics.mean(bytes_per_launch)),
             "mean_launch_us": round(statistics.mean(durs) * 1e3, 2),
         },
@@ -411,7 +411,7 @@ def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan):
 
 
 PROFILES = ROOT / "profiles"
-KERNEL_TAG = "page_copy_kernel<false>"
+KERNEL_TAG = "page_copy_kernel<false, false>"
 
 
 def _per_dispatch(csv_path: str, counter: str):
@@ -448,6 +448,128 @@ def summarize_pmc(fetch_csv: str, write_csv: str, workload: str) -> dict:
     return out
 
 
+def summarize_stats(stats_csv: str, bench_json: str, command: str) -> str:
+    """Markdown summary of a rocprofv3 --stats kernel table beside the bench
+    line of the same run (mean launch time measured with HIP events)."""
+    import csv
+
+    rows = list(csv.DictReader(open(stats_csv)))
+    bench = json.loads(open(bench_json).read())
+    cfg, rf = bench["config"], bench["roofline"]
+    out = [f"# page copy kernel on {cfg['workload']} - kernel trace statistics", "",
+           f"Workload: {cfg['description']}; {cfg['pages']} pages x {cfg['layers']} layers, "
+           f"payload {cfg['payload_bytes']} B.", "", "Command (repo root, one MI355X):", "", "```",
+           "export TMPDIR=/tmp", command, "```", "",
+           "| kernel | calls | average ns | min ns | max ns | std dev ns |", "|---|---|---|---|---|---|"]
+    for r in rows:
+        name = r["Name"]
+        if "pace_kv" in name:
+            short = name.replace("void pace_kv::(anonymous namespace)::", "").split("(")[0]
+        else:
+            short = "torch normal_ (pool fill)" if "distribution" in name else name[:48]
+        out.append(f"| {short} | {r['Calls']} | {float(r['AverageNs']):.0f} | {r['MinNs']} | {r['MaxNs']} | "
+                   f"{float(r['StdDev']):.0f} |")
+    pc = [r for r in rows if "page_copy_kernel" in r["Name"]]
+    if pc:
+        calls = sum(int(r["Calls"]) for r in pc)
+        avg_us = sum(float(r["AverageNs"]) * int(r["Calls"]) for r in pc) / calls / 1e3
+        per_launch = rf["algorithmic_bytes_per_launch"]
+        out += ["", f"bench.py in the same run (HIP events on the launch stream): mean launch "
+                f"{rf['mean_launch_us']} us, achieved {rf['achieved']} GB/s ({rf['frac'] * 100:.1f}% of 8 TB/s); "
+                f"headline value {bench['value']} GB/s.",
+                f"rocprofv3 average over {calls} page-copy launches {avg_us:.2f} us vs bench {rf['mean_launch_us']} us "
+                f"({(rf['mean_launch_us'] / avg_us - 1) * 100:+.2f}%); {per_launch} B / {avg_us:.2f} us = "
+                f"{per_launch / (avg_us * 1e-6) / 1e9:.0f} GB/s per launch."]
+    return "\n".join(out) + "\n"
+
+
+def summarize_copies(copy_csv: str, kernel_csv: str, bench_json: str, command: str) -> str:
+    """Markdown summary of the pinned-host round trip from a rocprofv3
+    --memory-copy-trace (DMA-engine copies) and --kernel-trace (the runtime
+    runs some device-to-host copies as __amd_rocclr_copyBuffer blit kernels):
+    per-direction busy time and how long both directions ran at once."""
+    import csv
+
+    bench = json.loads(open(bench_json).read())
+    st = bench.get("staging") or {}
+    chunk = int(st.get("chunk_bytes", 0))
+    spans = {"D2H": [], "H2D": []}
+    for r in csv.DictReader(open(copy_csv)):
+        d = "D2H" if "DEVICE_TO_HOST" in r["Direction"] else ("H2D" if "HOST_TO_DEVICE" in r["Direction"] else None)
+        if d:
+            spans[d].append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), "DMA engine"))
+    min_ns = 1_000_000   # blits shorter than 1 ms are not chunk copies
+    for r in csv.DictReader(open(kernel_csv)):
+        s0, e0 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        if "copyBuffer" in r["Kernel_Name"] and e0 - s0 > min_ns:
+            spans["D2H"].append((s0, e0, "blit kernel"))
+    k = int(st.get("chunks", 0))
+    last = {d: sorted(v)[-k:] for d, v in spans.items()}
+    t0 = min(v[0][0] for v in last.values() if v)
+    t1 = max(v[-1][1] for v in last.values() if v)
+
+    def busy(v):
+        return sum(e - s for s, e, _ in v)
+
+    both = sum(max(0, min(e1, e2) - max(s1, s2)) for s1, e1, _ in last["D2H"] for s2, e2, _ in last["H2D"])
+    out = ["# pinned-host round trip on " + bench["config"]["workload"] + " - memory copy trace", "",
+           bench["config"]["description"] + ".", "", "Command (repo root, one MI355X):", "", "```",
+           "export TMPDIR=/tmp", command, "```", "",
+           f"Last round trip: {k} chunks of {chunk} B each way (layers_per_chunk={st.get('layers_per_chunk')}), "
+           f"host ring {st.get('host_ring_bytes')} B.", "",
+           "| direction | copies | executed as | busy ms | mean GB/s while busy |", "|---|---|---|---|---|"]
+    for d in ("D2H", "H2D"):
+        v = last[d]
+        if v:
+            kinds = ", ".join(f"{sum(1 for x in v if x[2] == kd)} {kd}" for kd in sorted({x[2] for x in v}))
+            out.append(f"| {d} | {len(v)} | {kinds} | {busy(v) / 1e6:.2f} | "
+                       f"{len(v) * chunk / (busy(v) * 1e-9) / 1e9:.1f} |")
+    out += ["", f"Wall span of the last round trip: {(t1 - t0) / 1e6:.2f} ms; both directions busy at once for "
+            f"{both / 1e6:.2f} ms ({both / max(1, t1 - t0) * 100:.0f}% of the span).",
+            f"bench.py in the same run: round trip {st.get('roundtrip_ms')} ms = "
+            f"{st.get('roundtrip_gbs_per_direction')} GB/s per direction (PCIe Gen5 x16 peak 64 GB/s per direction)."]
+    return "\n".join(out) + "\n"
+
+
+def pmc_markdown(traffic_json: str) -> str:
+    """Markdown form of a --summarize-pmc result (the committed summary)."""
+    t = json.loads(open(traffic_json).read())
+    wl = t["workload"]
+    alg = None
+    try:
+        from paceserve_amd import workloads
+        w = workloads.config(int(wl.replace("config", "")))
+        alg = 2 * w.payload_bytes
+    except Exception:
+        pass
+    cmds = [
+        "export TMPDIR=/tmp",
+        "timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch -o f -- "
+        "python3 bench.py --no-cpu --no-promote --steps 3 --warmup 1 --calibrate",
+        "timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write -o w -- "
+        "python3 bench.py --no-cpu --no-promote --steps 3 --warmup 1 --calibrate",
+        "python3 bench.py --summarize-pmc gpurun_out/pmc_fetch/f_counter_collection.csv "
+        f"gpurun_out/pmc_write/w_counter_collection.csv {wl} > profiles/page_copy_{wl}_traffic.json",
+    ]
+    out = [f"# {t['kernel']} on {wl} - HBM traffic per launch (rocprofv3 PMC)", "",
+           "Commands (repo root, one MI355X; one counter per pass):", "", "```", *cmds, "```", "",
+           "`--calibrate` runs a device copy of 1 GiB three times in the same process (torch `copy_`, "
+           "dispatched as `__amd_rocclr_copyBuffer`): the reference dispatch of known size.", "",
+           f"| counter | page copy kernel, KiB per dispatch (raw, {t['fetch_dispatches']} dispatches) | "
+           "1 GiB copy, KiB (raw) | scale to 1 GiB | bytes per launch |", "|---|---|---|---|---|",
+           f"| FETCH_SIZE | {t['fetch_kib_per_dispatch_raw']:.1f} | {t['fetch_calibration_kib_raw']:.1f} | "
+           f"{t['fetch_scale']} | {t['fetch_bytes_per_launch']} |",
+           f"| WRITE_SIZE | {t['write_kib_per_dispatch_raw']:.1f} | {t['write_calibration_kib_raw']:.1f} | "
+           f"{t['write_scale']} | {t['write_bytes_per_launch']} |", ""]
+    if alg:
+        out += [f"Algorithmic bytes per launch: {alg} (payload read once, written once).",
+                f"Measured HBM traffic per launch: {t['traffic_bytes_per_launch']} B = "
+                f"{t['traffic_bytes_per_launch'] / alg:.5f} x algorithmic: no re-reads, no partial-line writes."]
+    out += ["(Counter collection serialises dispatches, so runs under --pmc report lower throughput; "
+            "only the byte counts are used.)"]
+    return "\n".join(out) + "\n"
+
+
 def traffic_from_profiles(workload: str):
     path = PROFILES / f"page_copy_{workload}_traffic.json"
     if not path.exists():
@@ -461,6 +583,18 @@ def main():
         # python bench.py --summarize-pmc FETCH.csv WRITE.csv WORKLOAD
         d = summarize_pmc(sys.argv[2], sys.argv[3], sys.argv[4])
         print(json.dumps(d, indent=1))
+        return
+    if len(sys.argv) > 1 and sys.argv[1] == "--pmc-markdown":
+        # python bench.py --pmc-markdown profiles/page_copy_WORKLOAD_traffic.json
+        print(pmc_markdown(sys.argv[2]), end="")
+        return
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-stats":
+        # python bench.py --summarize-stats KERNEL_STATS.csv BENCH_LINE.json "COMMAND"
+        print(summarize_stats(sys.argv[2], sys.argv[3], sys.argv[4]), end="")
+        return
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-copies":
+        # python bench.py --summarize-copies MEMORY_COPY_TRACE.csv KERNEL_TRACE.csv BENCH_LINE.json "COMMAND"
+        print(summarize_copies(sys.argv[2], sys.argv[3], sys.argv[4], sys.argv[5]), end="")
         return
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
