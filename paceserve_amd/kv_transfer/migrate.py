@@ -23,9 +23,11 @@ is byte-identical to what the reference's get_kv_cache returns for it.
 """
 from __future__ import annotations
 
+import itertools
 from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
+import numpy as np
 import torch
 
 from ..core.block_manager import BlockAllocator, NativeBlockAllocator, remap_dst_table
@@ -79,6 +81,26 @@ def plan_batch(src_tables: Sequence[Sequence[int]], src_num_pages: int, dst_allo
     return MigrationPlan(src_ids, dst_ids, dst_tables, indptr)
 
 
+def flatten_tables(src_tables: Sequence[Sequence[int]], num_pages: int):
+    """CSR form of a batch of source block tables: (ids int32, indptr int64,
+    counts).  Ids follow torch advanced-indexing rules, as normalize_page_ids
+    does: negative ids count from the end, and an id outside
+    [-num_pages, num_pages) raises IndexError."""
+    counts = [len(t) for t in src_tables]
+    indptr = np.array([0, *itertools.accumulate(counts)], dtype=np.int64)
+    total = int(indptr[-1])
+    ids = src_tables[0] if len(counts) == 1 else itertools.chain.from_iterable(src_tables)
+    flat = np.fromiter(ids, dtype=np.int64, count=total)
+    if total:
+        lo, hi = int(flat.min()), int(flat.max())
+        if lo < -num_pages or hi >= num_pages:
+            bad = flat[(flat < -num_pages) | (flat >= num_pages)][0]
+            raise IndexError(f"index {bad} is out of bounds for dimension 0 with size {num_pages}")
+        if lo < 0:
+            flat = np.where(flat < 0, flat + num_pages, flat)
+    return flat.astype(np.int32), indptr, counts
+
+
 class KVMigrator:
     def __init__(self, src, dst, dst_allocator: BlockAllocator, *,
                  buffer_bytes_max: int = 8 << 30, stager: Optional[ops.Stager] = None):
@@ -90,6 +112,8 @@ class KVMigrator:
         self.buffer_bytes_max = int(buffer_bytes_max)
         self.stager = stager
         self._buf: Optional[torch.Tensor] = None
+        self._buf_view: Optional[torch.Tensor] = None
+        self._elem = self.src.layers[0].element_size()
         self._promoter: Optional[ops.Promoter] = None
 
     # ------------------------------------------------------------ planning
@@ -111,11 +135,18 @@ class KVMigrator:
     # ------------------------------------------------------------ movement
 
     def _buffer(self, layers: int, n: int) -> torch.Tensor:
+        """A [layers, n, *page_shape] view of the migrator's transfer buffer
+        (grown on demand; the last view is reused for the same shape)."""
+        v = self._buf_view
+        if v is not None and v.shape[0] == layers and v.shape[1] == n:
+            return v
         need = (layers, n) + self.src.page_shape
-        numel = layers * n * self.src.page_bytes // torch.empty(0, dtype=self.src.dtype).element_size()
+        numel = layers * n * self.src.page_bytes // self._elem
         if self._buf is None or self._buf.numel() < numel:
+            self._buf_view = None
             self._buf = torch.empty(numel, dtype=self.src.dtype, device=self.src.device)
-        return self._buf[:numel].view(need)
+        self._buf_view = self._buf[:numel].view(need)
+        return self._buf_view
 
     def chunk_layers(self, n: int) -> int:
         layer_bytes = max(1, n * self.src.page_bytes)
@@ -178,19 +209,9 @@ class KVMigrator:
         work is enqueued on the current stream (synchronize to wait).  With a
         NativeBlockAllocator, the device modes run as one library call."""
         if isinstance(self.dst_allocator, NativeBlockAllocator) and mode in ("buffer", "fused"):
-            import itertools
-
-            import numpy as np
-            counts = [len(t) for t in src_tables]
-            indptr = np.zeros(len(counts) + 1, dtype=np.int64)
-            np.cumsum(counts, out=indptr[1:])
-            flat = np.fromiter(itertools.chain.from_iterable(src_tables), dtype=np.int64,
-                               count=int(indptr[-1]))
-            npages = self.src.num_pages
-            if flat.size and (flat.min() < -npages or flat.max() >= npages):
-                bad = flat[(flat < -npages) | (flat >= npages)][0]
-                raise IndexError(f"index {bad} is out of bounds for dimension 0 with size {npages}")
-            src_ids = np.where(flat < 0, flat + npages, flat).astype(np.int32)
+            # Only the work before the library call adds latency: the plan
+            # below is built while the GPU copies.
+            src_ids, indptr, counts = flatten_tables(src_tables, self.src.num_pages)
             tables = self.promote_native(src_ids, indptr, dst_pages, mode, layers_per_chunk).tolist()
             sizes = counts if dst_pages is None else list(dst_pages)
             dst_tables, dst_ids, pos = [], [], 0

@@ -258,14 +258,18 @@ class Promoter:
         import numpy as np
 
         sp, dp = as_pool(src), as_pool(dst)
-        if not sp.compatible(dp) or sp.num_layers != dp.num_layers:
+        if sp is not dp and (not sp.compatible(dp) or sp.num_layers != dp.num_layers):
             raise ValueError("source and destination pools differ in layout, layers, dtype or device")
         if self._handle is None:
             raise RuntimeError("promoter is closed")
         src_ids = np.ascontiguousarray(src_ids, dtype=np.int32)
         indptr = np.ascontiguousarray(indptr, dtype=np.int64)
-        counts = np.diff(indptr) if dst_pages is None else np.ascontiguousarray(dst_pages, dtype=np.int32)
-        total = int(counts.sum())
+        if dst_pages is None:
+            counts = None
+            total = int(indptr[-1]) if indptr.size else 0
+        else:
+            counts = np.ascontiguousarray(dst_pages, dtype=np.int32)
+            total = int(counts.sum())
         tables = np.empty(max(total, 1), dtype=np.int32)
         buf_ptr, stride, blayers = None, 0, 0
         if buffer is not None:

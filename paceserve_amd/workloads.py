@@ -47,6 +47,10 @@ class KVShape:
         return (2, self.page_size, self.num_kv_heads, self.head_dim)
 
     @property
+    def dtype_name(self) -> str:
+        return str(self.dtype).replace("torch.", "")
+
+    @property
     def page_bytes(self) -> int:
         return 2 * self.page_size * self.num_kv_heads * self.head_dim * torch.empty(0, dtype=self.dtype).element_size()
 

@@ -8,7 +8,7 @@ from paceserve_amd.core.block_manager import BlockAllocator, BlockSpaceManager, 
 from paceserve_amd.core.kv_cache_obj import KVobj
 from paceserve_amd.core.sequence import Sequence
 from paceserve_amd.kv_transfer.kv_utils import chunk_layers, dedup_keep_last, normalize_page_ids
-from paceserve_amd.kv_transfer.migrate import plan_batch
+from paceserve_amd.kv_transfer.migrate import flatten_tables, plan_batch
 from paceserve_amd.kv_transfer.worker import KVStatus, KVWorker, WorkerSequenceManager
 
 
@@ -106,6 +106,24 @@ def test_normalize_and_dedup_follow_torch_semantics():
     keep = dedup_keep_last(ids)
     pos, kept = orc.dedup_keep_last(ids, 4)
     assert keep == pos.tolist() and [ids[p] for p in keep] == kept.tolist()
+
+
+def test_flatten_tables_matches_per_request_normalization():
+    rng = np.random.default_rng(5)
+    tables = [rng.integers(-64, 64, int(k)).tolist() for k in rng.integers(0, 20, 9)]
+    ids, indptr, counts = flatten_tables(tables, 64)
+    assert ids.dtype == np.int32 and indptr.dtype == np.int64
+    assert counts == [len(t) for t in tables]
+    assert indptr.tolist() == [0] + np.cumsum(counts).tolist()
+    for r, t in enumerate(tables):
+        assert ids[indptr[r]:indptr[r + 1]].tolist() == normalize_page_ids(t, 64)
+    one, ip, _ = flatten_tables([[3, -1]], 8)
+    assert one.tolist() == [3, 7] and ip.tolist() == [0, 2]
+    empty, ip, _ = flatten_tables([], 8)
+    assert empty.size == 0 and ip.tolist() == [0]
+    for bad in ([[0, 8]], [[1], [-9]]):
+        with pytest.raises(IndexError, match="out of bounds for dimension 0 with size 8"):
+            flatten_tables(bad, 8)
 
 
 def test_chunk_layers():
