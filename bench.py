@@ -202,6 +202,7 @@ def run_device(args, w, dev, src, dst, plan, s_ids, d_ids):
             "launch_timing": "HIP events around the K timed steps on the launch stream, divided by "
                              "the launches they hold",
             "evented_launch_us": round(statistics.mean(durs) * 1e3, 2),
+            "launches_per_step": launches_per_step,
         },
     }
     return res
@@ -512,9 +513,27 @@ def summarize_pmc(fetch_csv: str, write_csv: str, workload: str) -> dict:
     return out
 
 
-def summarize_stats(stats_csv: str, bench_json: str, command: str) -> str:
+def timed_dispatches(trace_csv: str, bench: dict):
+    """The page-copy dispatches of the timed steps in a rocprofv3 kernel
+    trace of one bench.py run: page-copy launches in dispatch order are the
+    W warm-up steps, then the K timed steps, then the launch-timing pass and
+    the copy-ceiling run; returns (durations ns, span ns) of the timed ones."""
+    import csv
+
+    rows = [r for r in csv.DictReader(open(trace_csv)) if "page_copy_kernel" in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    per_step = bench["roofline"]["launches_per_step"]
+    first = bench["warmup"] * per_step
+    timed = rows[first:first + bench["steps"] * per_step]
+    durs = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in timed]
+    span = int(timed[-1]["End_Timestamp"]) - int(timed[0]["Start_Timestamp"])
+    return durs, span
+
+
+def summarize_stats(stats_csv: str, bench_json: str, command: str, trace_csv: str = "") -> str:
     """Markdown summary of a rocprofv3 --stats kernel table beside the bench
-    line of the same run (mean launch time measured with HIP events)."""
+    line of the same run (mean launch time measured with HIP events); with
+    the kernel trace, also the timed steps' own dispatches."""
     import csv
 
     rows = list(csv.DictReader(open(stats_csv)))
@@ -541,9 +560,16 @@ def summarize_stats(stats_csv: str, bench_json: str, command: str) -> str:
         out += ["", f"bench.py in the same run (HIP events on the launch stream): mean launch "
                 f"{rf['mean_launch_us']} us, achieved {rf['achieved']} GB/s ({rf['frac'] * 100:.1f}% of 8 TB/s); "
                 f"headline value {bench['value']} GB/s.",
-                f"rocprofv3 average over {calls} page-copy launches {avg_us:.2f} us vs bench {rf['mean_launch_us']} us "
-                f"({(rf['mean_launch_us'] / avg_us - 1) * 100:+.2f}%); {per_launch} B / {avg_us:.2f} us = "
-                f"{per_launch / (avg_us * 1e-6) / 1e9:.0f} GB/s per launch."]
+                f"rocprofv3 average over all {calls} page-copy launches of the run (warm-up, timed steps, "
+                f"launch-timing pass, copy ceiling) {avg_us:.2f} us."]
+        if trace_csv:
+            durs, span = timed_dispatches(trace_csv, bench)
+            mean_us = statistics.mean(durs) / 1e3
+            span_us = span / 1e3 / len(durs)
+            out += [f"Timed steps only ({len(durs)} launches, from the kernel trace): mean kernel duration "
+                    f"{mean_us:.2f} us ({per_launch / (mean_us * 1e-6) / 1e9:.0f} GB/s per launch); first start to "
+                    f"last end {span_us:.2f} us per launch vs bench {rf['mean_launch_us']} us "
+                    f"({(rf['mean_launch_us'] / span_us - 1) * 100:+.2f}%)."]
     return "\n".join(out) + "\n"
 
 
@@ -653,8 +679,8 @@ def main():
         print(pmc_markdown(sys.argv[2]), end="")
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-stats":
-        # python bench.py --summarize-stats KERNEL_STATS.csv BENCH_LINE.json "COMMAND"
-        print(summarize_stats(sys.argv[2], sys.argv[3], sys.argv[4]), end="")
+        # python bench.py --summarize-stats KERNEL_STATS.csv BENCH_LINE.json "COMMAND" [KERNEL_TRACE.csv]
+        print(summarize_stats(*sys.argv[2:6]), end="")
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-copies":
         # python bench.py --summarize-copies MEMORY_COPY_TRACE.csv KERNEL_TRACE.csv BENCH_LINE.json "COMMAND"
