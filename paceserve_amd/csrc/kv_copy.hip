@@ -12,10 +12,13 @@
 // Work decomposition.  A page of one layer is `page_bytes` contiguous bytes
 // (K half then V half).  It is split into 1 KiB rows; one workgroup of one
 // wave64 copies one row, each lane moving one 16-byte vector with a
-// nontemporal load and a nontemporal store, and then retires.  Work items are
-// ordered layer-major, then page, then row, so workgroups dispatched together
-// read (unpack) or write (pack) adjacent rows of the transfer buffer and
-// adjacent rows of each pool page.  Measured on MI355X, this fine grain keeps
+// nontemporal load and a nontemporal store, and then retires.  The grid is
+// rows x pages x layers (blockIdx.x = row, .y = page, .z = layer), so a wave
+// finds its row without integer division, and workgroups, dispatched row
+// fastest, then page, then layer, read (unpack) or write (pack) adjacent rows
+// of the transfer buffer and adjacent rows of each pool page.  An unpack wave
+// issues its buffer load before its destination page id arrives.  Measured on
+// MI355X, this fine grain keeps
 // the chip's in-flight accesses within a narrow address window and copies at
 // ~6.6 TB/s, against ~5.6-5.9 TB/s for 8-32 KiB per workgroup, persistent
 // grid-stride loops or ids staged in LDS (a persistent loop serialises each
@@ -47,6 +50,9 @@ constexpr int64_t kTemporalStoreMaxBytes = int64_t(1) << 30;
 // Workgroups per launch stay below 2^25 so that grid * 64 threads fits the
 // 32-bit launch limit with room to spare; larger batches use more launches.
 constexpr int64_t kMaxItemsPerLaunch = int64_t(1) << 25;
+// Pages per launch: the grid's y dimension (a batch with more pages uses
+// more launches).
+constexpr int64_t kMaxPagesPerLaunch = 65535;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -61,9 +67,6 @@ struct CopyParams {
   int64_t page_bytes;
   uint32_t src_pool_pages;
   uint32_t dst_pool_pages;
-  uint32_t n_pages;
-  uint32_t rows_per_page;  // ceil(page_bytes / kRowBytes)
-  uint32_t total_items;    // layers * n_pages * rows_per_page (== grid size)
   uint32_t page_vecs;      // page_bytes / 16
 };
 
@@ -79,86 +82,101 @@ __device__ __forceinline__ uint32_t page_of(const int32_t* ids, uint32_t j) {
   return ids ? static_cast<uint32_t>(ids[j]) : j;
 }
 
-// The copy of one 1 KiB row; shared by both id sources.  Loads are always
-// nontemporal; TEMPORAL selects plain stores (kept in the memory-side cache)
-// instead of nontemporal ones.
+template <bool TEMPORAL>
+__device__ __forceinline__ void store_vec(const u32x4 v, u32x4* d) {
+  if (TEMPORAL) *d = v;
+  else __builtin_nontemporal_store(v, d);
+}
+
+// The copy of one 1 KiB row: row blockIdx.x of page blockIdx.y of layer
+// blockIdx.z (the grid is exactly rows x pages x layers, dispatched row
+// fastest).  sids / dids are the sides' page ids (device or kernel-argument
+// arrays), nullptr for a contiguous side.  Loads are always nontemporal;
+// TEMPORAL selects plain stores (kept in the memory-side cache) instead of
+// nontemporal ones.
 template <bool GUARD, bool TEMPORAL>
-__device__ __forceinline__ void copy_row(const CopyParams& p, uint32_t item, bool inline_ids,
-                                         const int32_t* isrc, const int32_t* idst) {
-  const uint32_t page_linear = item / p.rows_per_page;
-  const uint32_t row = item - page_linear * p.rows_per_page;
-  const uint32_t layer = page_linear / p.n_pages;
-  const uint32_t j = page_linear - layer * p.n_pages;
-  const uint32_t sp = inline_ids ? page_of(isrc, j) : page_of(p.src_ids, j);
-  const uint32_t dp = inline_ids ? page_of(idst, j) : page_of(p.dst_ids, j);
+__device__ __forceinline__ void copy_row(const CopyParams& p, const int32_t* sids,
+                                         const int32_t* dids) {
+  const uint32_t row = blockIdx.x;
+  const uint32_t j = blockIdx.y;
+  const uint32_t layer = blockIdx.z;
+  const uint32_t vec = row * kThreads + threadIdx.x;
+  // Lane 0 of row 0 is never guarded out, so a skipped tile is still counted.
+  if (GUARD && vec >= p.page_vecs) return;
+  if (sids == nullptr) {
+    // Contiguous source (unpack): page j of the buffer is always in bounds,
+    // so the load is issued before the destination id is known.
+    const u32x4 v = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4*>(p.src[layer] + static_cast<int64_t>(j) * p.page_bytes) + vec);
+    const uint32_t dp = page_of(dids, j);
+    if (dp >= p.dst_pool_pages) {
+      if (row == 0 && threadIdx.x == 0 && p.err != nullptr) atomicAdd(p.err, 1);
+      return;
+    }
+    store_vec<TEMPORAL>(v, reinterpret_cast<u32x4*>(p.dst[layer] + static_cast<int64_t>(dp) * p.page_bytes) + vec);
+    return;
+  }
+  const uint32_t sp = static_cast<uint32_t>(sids[j]);
+  const uint32_t dp = page_of(dids, j);
   // Negative ids wrap to large unsigned values and fail the same test.
   if (sp >= p.src_pool_pages || dp >= p.dst_pool_pages) {
     if (row == 0 && threadIdx.x == 0 && p.err != nullptr) atomicAdd(p.err, 1);
     return;
   }
-  const uint32_t vec = row * kThreads + threadIdx.x;
-  if (GUARD && vec >= p.page_vecs) return;
-  const u32x4* s = reinterpret_cast<const u32x4*>(
-                       p.src[layer] + static_cast<int64_t>(sp) * p.page_bytes) + vec;
-  u32x4* d = reinterpret_cast<u32x4*>(
-                 p.dst[layer] + static_cast<int64_t>(dp) * p.page_bytes) + vec;
-  const u32x4 v = __builtin_nontemporal_load(s);
-  if (TEMPORAL) *d = v;
-  else __builtin_nontemporal_store(v, d);
+  const u32x4 v = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4*>(p.src[layer] + static_cast<int64_t>(sp) * p.page_bytes) + vec);
+  store_vec<TEMPORAL>(v, reinterpret_cast<u32x4*>(p.dst[layer] + static_cast<int64_t>(dp) * p.page_bytes) + vec);
 }
 
 // GUARD: page_bytes is not a multiple of kRowBytes, so the last row of a page
 // is partial.
 template <bool GUARD, bool TEMPORAL>
 __global__ __launch_bounds__(kThreads) void page_copy_kernel(const CopyParams p) {
-  const uint32_t item = blockIdx.x;
-  if (item >= p.total_items) return;
-  copy_row<GUARD, TEMPORAL>(p, item, false, nullptr, nullptr);
+  copy_row<GUARD, TEMPORAL>(p, p.src_ids, p.dst_ids);
 }
 
 // Same copy with the ids in the kernel arguments.  A side whose ids are not
-// inline (the contiguous buffer of a pack or unpack) is marked by a null
-// pointer in the base parameters and indexes pages by position.
+// inline (the contiguous buffer of a pack or unpack) indexes pages by
+// position.
 template <bool GUARD, bool TEMPORAL, bool SRC_INLINE, bool DST_INLINE>
 __global__ __launch_bounds__(kThreads) void page_copy_inline_kernel(const CopyParamsInline p) {
-  const uint32_t item = blockIdx.x;
-  if (item >= p.base.total_items) return;
-  copy_row<GUARD, TEMPORAL>(p.base, item, true, SRC_INLINE ? p.src_ids : nullptr,
-                            DST_INLINE ? p.dst_ids : nullptr);
+  copy_row<GUARD, TEMPORAL>(p.base, SRC_INLINE ? p.src_ids : nullptr, DST_INLINE ? p.dst_ids : nullptr);
 }
 
 template <bool GUARD, bool TEMPORAL>
-hipError_t launch_t(const CopyParams& p, hipStream_t stream) {
+hipError_t launch_t(const CopyParams& p, dim3 grid, hipStream_t stream) {
   void* args[] = {const_cast<CopyParams*>(&p)};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&page_copy_kernel<GUARD, TEMPORAL>),
-                         dim3(p.total_items), dim3(kThreads), args, 0, stream);
+  return hipLaunchKernel(reinterpret_cast<const void*>(&page_copy_kernel<GUARD, TEMPORAL>), grid,
+                         dim3(kThreads), args, 0, stream);
 }
 
-hipError_t launch(const CopyParams& p, bool guard, bool temporal, hipStream_t stream) {
-  if (guard) return temporal ? launch_t<true, true>(p, stream) : launch_t<true, false>(p, stream);
-  return temporal ? launch_t<false, true>(p, stream) : launch_t<false, false>(p, stream);
+hipError_t launch(const CopyParams& p, dim3 grid, bool guard, bool temporal, hipStream_t stream) {
+  if (guard) return temporal ? launch_t<true, true>(p, grid, stream) : launch_t<true, false>(p, grid, stream);
+  return temporal ? launch_t<false, true>(p, grid, stream) : launch_t<false, false>(p, grid, stream);
 }
 
 template <bool GUARD, bool TEMPORAL, bool S, bool D>
-hipError_t launch_inline_t(const CopyParamsInline& p, hipStream_t stream) {
+hipError_t launch_inline_t(const CopyParamsInline& p, dim3 grid, hipStream_t stream) {
   void* args[] = {const_cast<CopyParamsInline*>(&p)};
   return hipLaunchKernel(
-      reinterpret_cast<const void*>(&page_copy_inline_kernel<GUARD, TEMPORAL, S, D>),
-      dim3(p.base.total_items), dim3(kThreads), args, 0, stream);
+      reinterpret_cast<const void*>(&page_copy_inline_kernel<GUARD, TEMPORAL, S, D>), grid,
+      dim3(kThreads), args, 0, stream);
 }
 
 template <bool GUARD, bool TEMPORAL>
-hipError_t launch_inline_g(const CopyParamsInline& p, bool s, bool d, hipStream_t stream) {
-  if (s && d) return launch_inline_t<GUARD, TEMPORAL, true, true>(p, stream);
-  if (s) return launch_inline_t<GUARD, TEMPORAL, true, false>(p, stream);
-  return launch_inline_t<GUARD, TEMPORAL, false, true>(p, stream);
+hipError_t launch_inline_g(const CopyParamsInline& p, dim3 grid, bool s, bool d, hipStream_t stream) {
+  if (s && d) return launch_inline_t<GUARD, TEMPORAL, true, true>(p, grid, stream);
+  if (s) return launch_inline_t<GUARD, TEMPORAL, true, false>(p, grid, stream);
+  return launch_inline_t<GUARD, TEMPORAL, false, true>(p, grid, stream);
 }
 
-hipError_t launch_inline(const CopyParamsInline& p, bool guard, bool temporal, bool s, bool d,
-                         hipStream_t stream) {
+hipError_t launch_inline(const CopyParamsInline& p, dim3 grid, bool guard, bool temporal, bool s,
+                         bool d, hipStream_t stream) {
   if (guard)
-    return temporal ? launch_inline_g<true, true>(p, s, d, stream) : launch_inline_g<true, false>(p, s, d, stream);
-  return temporal ? launch_inline_g<false, true>(p, s, d, stream) : launch_inline_g<false, false>(p, s, d, stream);
+    return temporal ? launch_inline_g<true, true>(p, grid, s, d, stream)
+                    : launch_inline_g<true, false>(p, grid, s, d, stream);
+  return temporal ? launch_inline_g<false, true>(p, grid, s, d, stream)
+                  : launch_inline_g<false, false>(p, grid, s, d, stream);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -217,6 +235,10 @@ int launch_page_copy(const Side& src, const Side& dst, int num_layers, int64_t n
   rc = check_layers(dst.layers, num_layers, "destination");
   if (rc) return rc;
   const bool inline_ids = host_src_ids != nullptr || host_dst_ids != nullptr;
+  // The inline kernels index a side without inline ids by position.
+  if (inline_ids && ((host_src_ids == nullptr && src.ids != nullptr) ||
+                     (host_dst_ids == nullptr && dst.ids != nullptr)))
+    return fail(PACE_KV_EINVAL, "a launch cannot mix device and kernel-argument page ids");
   if (inline_ids && n_pages > PACE_KV_INLINE_IDS)
     return fail(PACE_KV_ERANGE, "more than %d pages cannot travel in the kernel arguments",
                 PACE_KV_INLINE_IDS);
@@ -234,7 +256,8 @@ int launch_page_copy(const Side& src, const Side& dst, int num_layers, int64_t n
 
   for (int l0 = 0; l0 < num_layers; l0 += kMaxLayers) {
     const int nl = num_layers - l0 < kMaxLayers ? num_layers - l0 : kMaxLayers;
-    const int64_t max_pages = kMaxItemsPerLaunch / (int64_t(nl) * rows_per_page);
+    int64_t max_pages = kMaxItemsPerLaunch / (int64_t(nl) * rows_per_page);
+    if (max_pages > kMaxPagesPerLaunch) max_pages = kMaxPagesPerLaunch;
     if (max_pages < 1)
       return fail(PACE_KV_ERANGE, "page_bytes too large for one launch (%lld)", (long long)page_bytes);
     for (int64_t j0 = 0; j0 < n_pages; j0 += max_pages) {
@@ -251,10 +274,9 @@ int launch_page_copy(const Side& src, const Side& dst, int num_layers, int64_t n
       p.page_bytes = page_bytes;
       p.src_pool_pages = src_indexed ? clamp_pool(src.pool_pages) : static_cast<uint32_t>(nj);
       p.dst_pool_pages = dst_indexed ? clamp_pool(dst.pool_pages) : static_cast<uint32_t>(nj);
-      p.n_pages = static_cast<uint32_t>(nj);
-      p.rows_per_page = static_cast<uint32_t>(rows_per_page);
-      p.total_items = static_cast<uint32_t>(int64_t(nl) * nj * rows_per_page);
       p.page_vecs = static_cast<uint32_t>(page_bytes / kVecBytes);
+      const dim3 grid(static_cast<uint32_t>(rows_per_page), static_cast<uint32_t>(nj),
+                      static_cast<uint32_t>(nl));
       const bool temporal = policy == StorePolicy::kTemporalIfSmall &&
                             int64_t(nl) * nj * page_bytes <= kTemporalStoreMaxBytes;
       if (inline_ids) {
@@ -262,11 +284,11 @@ int launch_page_copy(const Side& src, const Side& dst, int num_layers, int64_t n
         q.base = p;
         if (host_src_ids) memcpy(q.src_ids, host_src_ids + j0, nj * sizeof(int32_t));
         if (host_dst_ids) memcpy(q.dst_ids, host_dst_ids + j0, nj * sizeof(int32_t));
-        rc = hip_status(launch_inline(q, guard, temporal, host_src_ids != nullptr,
+        rc = hip_status(launch_inline(q, grid, guard, temporal, host_src_ids != nullptr,
                                       host_dst_ids != nullptr, stream),
                         "page copy launch");
       } else {
-        rc = hip_status(launch(p, guard, temporal, stream), "page copy launch");
+        rc = hip_status(launch(p, grid, guard, temporal, stream), "page copy launch");
       }
       if (rc) return rc;
     }

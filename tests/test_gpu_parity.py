@@ -156,6 +156,28 @@ def test_out_of_range_ids_are_skipped_and_counted(gpu):
         assert same(dst[l][keep], before[l][keep])
 
 
+def test_batches_over_65535_pages_split_across_launches(gpu):
+    # 128-byte pages (a partial 1 KiB row each): 131 073 pages take three
+    # launches per layer chunk on the grid's page dimension.
+    L, pages, shape, n = 2, 140_000, (2, 4, 1, 8), 131_073
+    src = rand_pool(L, pages, shape, torch.float16, gpu, 11)
+    dst = rand_pool(L, pages, shape, torch.float16, gpu, 12)
+    g = torch.Generator(device=gpu).manual_seed(13)
+    s_ids = torch.randperm(pages, generator=g, device=gpu)[:n].to(torch.int32)
+    d_ids = torch.randperm(pages, generator=g, device=gpu)[:n].to(torch.int32)
+    want = [d.clone() for d in dst]
+    for l in range(L):
+        words(want[l]).index_copy_(0, d_ids.long(), words(src[l]).index_select(0, s_ids.long()))
+    buf = ops.pack(src, s_ids)
+    fused = [d.clone() for d in dst]
+    ops.unpack(buf, dst, d_ids)
+    ops.move(src, s_ids, fused, d_ids)
+    torch.cuda.synchronize()
+    for l in range(L):
+        assert same(buf[l], src[l].index_select(0, s_ids.long()))
+        assert same(dst[l], want[l]) and same(fused[l], want[l])
+
+
 def test_empty_batch_is_a_no_op(gpu):
     src = rand_pool(2, 4, (2, 16, 8, 128), torch.float16, gpu, 4)
     buf = ops.pack(src, [])
