@@ -62,6 +62,8 @@ def parse_args():
                     help="after timing, run torch's contiguous copy of 1 GiB three times (PMC scale reference)")
     ap.add_argument("--staging", action="store_true",
                     help="also time the pinned-host round trip (default for workloads 3 and 4)")
+    ap.add_argument("--no-staging", action="store_true",
+                    help="skip the pinned-host round trip, also for workloads 3 and 4")
     return ap.parse_args()
 
 
@@ -625,21 +627,21 @@ def pmc_markdown(traffic_json: str) -> str:
     """Markdown form of a --summarize-pmc result (the committed summary)."""
     t = json.loads(open(traffic_json).read())
     wl = t["workload"]
-    alg = None
-    try:
-        from paceserve_amd import workloads
-        w = workloads.config(int(wl.replace("config", "")))
-        alg = 2 * w.payload_bytes
-    except Exception:
-        pass
+    from paceserve_amd import workloads
+
+    c = wl.replace("config", "")
+    w = workloads.config(int(c))
+    # one launch reads and writes its layer chunk's pages once
+    chunk = min(w.device_layers_per_chunk or w.shape.num_layers, w.shape.num_layers)
+    alg = 2 * chunk * w.n_pages * w.shape.page_bytes
+    run = f"python3 bench.py --workload {c} --no-cpu --no-promote --no-staging --steps 3 --warmup 1 --calibrate"
     cmds = [
         "export TMPDIR=/tmp",
-        "timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch -o f -- "
-        "python3 bench.py --no-cpu --no-promote --steps 3 --warmup 1 --calibrate",
-        "timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write -o w -- "
-        "python3 bench.py --no-cpu --no-promote --steps 3 --warmup 1 --calibrate",
-        "python3 bench.py --summarize-pmc gpurun_out/pmc_fetch/f_counter_collection.csv "
-        f"gpurun_out/pmc_write/w_counter_collection.csv {wl} > profiles/page_copy_{wl}_traffic.json",
+        f"timeout -s KILL 300 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch_{wl} -o f -- {run}",
+        f"timeout -s KILL 300 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write_{wl} -o w -- {run}",
+        f"python3 bench.py --summarize-pmc gpurun_out/pmc_fetch_{wl}/f_counter_collection.csv "
+        f"gpurun_out/pmc_write_{wl}/w_counter_collection.csv {wl} > profiles/page_copy_{wl}_traffic.json",
+        f"python3 bench.py --pmc-markdown profiles/page_copy_{wl}_traffic.json > profiles/page_copy_{wl}_traffic.md",
     ]
     out = [f"# {t['kernel']} on {wl} - HBM traffic per launch (rocprofv3 PMC)", "",
            "Commands (repo root, one MI355X; one counter per pass):", "", "```", *cmds, "```", "",
@@ -652,7 +654,8 @@ def pmc_markdown(traffic_json: str) -> str:
            f"| WRITE_SIZE | {t['write_kib_per_dispatch_raw']:.1f} | {t['write_calibration_kib_raw']:.1f} | "
            f"{t['write_scale']} | {t['write_bytes_per_launch']} |", ""]
     if alg:
-        out += [f"Algorithmic bytes per launch: {alg} (payload read once, written once).",
+        out += [f"Algorithmic bytes per launch: {alg} ({chunk} layers x {w.n_pages} pages x {w.shape.page_bytes} B, "
+                "read once and written once).",
                 f"Measured HBM traffic per launch: {t['traffic_bytes_per_launch']} B = "
                 f"{t['traffic_bytes_per_launch'] / alg:.5f} x algorithmic: no re-reads, no partial-line writes."]
     out += ["(Counter collection serialises dispatches, so runs under --pmc report lower throughput; "
@@ -721,10 +724,11 @@ def main():
     # frees make the driver scrub memory with the same DMA engines.
     staging = None
     promote = None
-    if args.staging or w.staging in ("pinned", "both") or not args.no_promote:
+    want_staging = not args.no_staging and (args.staging or w.staging in ("pinned", "both"))
+    if want_staging or not args.no_promote:
         settle = link_settle(dev)
         log(f"host link settled after {settle['waited_s']} s at {settle['d2h_gbs']} GB/s D2H")
-        if args.staging or w.staging in ("pinned", "both"):
+        if want_staging:
             staging = run_staging(w, dev, src, dst, s_ids, d_ids)
             staging["link_probe"] = settle
             if args.verify:
