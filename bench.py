@@ -474,14 +474,24 @@ def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan):
 
 
 PROFILES = ROOT / "profiles"
+
+
+def _rows(csv_path: str) -> list:
+    import csv
+
+    with open(csv_path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _json(path: str) -> dict:
+    with open(path) as f:
+        return json.load(f)
 KERNEL_TAG = "page_copy_kernel<false, false>"
 
 
 def _per_dispatch(csv_path: str, counter: str):
-    import csv
-
     by = {}
-    for r in csv.DictReader(open(csv_path)):
+    for r in _rows(csv_path):
         if r["Counter_Name"] != counter:
             continue
         by.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
@@ -520,9 +530,7 @@ def timed_dispatches(trace_csv: str, bench: dict):
     trace of one bench.py run: page-copy launches in dispatch order are the
     W warm-up steps, then the K timed steps, then the launch-timing pass and
     the copy-ceiling run; returns (durations ns, span ns) of the timed ones."""
-    import csv
-
-    rows = [r for r in csv.DictReader(open(trace_csv)) if "page_copy_kernel" in r["Kernel_Name"]]
+    rows = [r for r in _rows(trace_csv) if "page_copy_kernel" in r["Kernel_Name"]]
     rows.sort(key=lambda r: int(r["Dispatch_Id"]))
     per_step = bench["roofline"]["launches_per_step"]
     first = bench["warmup"] * per_step
@@ -536,10 +544,8 @@ def summarize_stats(stats_csv: str, bench_json: str, command: str, trace_csv: st
     """Markdown summary of a rocprofv3 --stats kernel table beside the bench
     line of the same run (mean launch time measured with HIP events); with
     the kernel trace, also the timed steps' own dispatches."""
-    import csv
-
-    rows = list(csv.DictReader(open(stats_csv)))
-    bench = json.loads(open(bench_json).read())
+    rows = _rows(stats_csv)
+    bench = _json(bench_json)
     cfg, rf = bench["config"], bench["roofline"]
     out = [f"# page copy kernel on {cfg['workload']} - kernel trace statistics", "",
            f"Workload: {cfg['description']}; {cfg['pages']} pages x {cfg['layers']} layers, "
@@ -580,18 +586,16 @@ def summarize_copies(copy_csv: str, kernel_csv: str, bench_json: str, command: s
     --memory-copy-trace (DMA-engine copies) and --kernel-trace (the runtime
     runs some device-to-host copies as __amd_rocclr_copyBuffer blit kernels):
     per-direction busy time and how long both directions ran at once."""
-    import csv
-
-    bench = json.loads(open(bench_json).read())
+    bench = _json(bench_json)
     st = bench.get("staging") or {}
     chunk = int(st.get("chunk_bytes", 0))
     spans = {"D2H": [], "H2D": []}
-    for r in csv.DictReader(open(copy_csv)):
+    for r in _rows(copy_csv):
         d = "D2H" if "DEVICE_TO_HOST" in r["Direction"] else ("H2D" if "HOST_TO_DEVICE" in r["Direction"] else None)
         if d:
             spans[d].append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), "DMA engine"))
     min_ns = 1_000_000   # blits shorter than 1 ms are not chunk copies
-    for r in csv.DictReader(open(kernel_csv)):
+    for r in _rows(kernel_csv):
         s0, e0 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
         if "copyBuffer" in r["Kernel_Name"] and e0 - s0 > min_ns:
             spans["D2H"].append((s0, e0, "blit kernel"))
@@ -625,7 +629,7 @@ def summarize_copies(copy_csv: str, kernel_csv: str, bench_json: str, command: s
 
 def pmc_markdown(traffic_json: str) -> str:
     """Markdown form of a --summarize-pmc result (the committed summary)."""
-    t = json.loads(open(traffic_json).read())
+    t = _json(traffic_json)
     wl = t["workload"]
     from paceserve_amd import workloads
 

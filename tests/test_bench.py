@@ -1,0 +1,102 @@
+"""bench.py's measurement helpers on synthetic profiler output (no GPU):
+kernel naming, PMC byte scaling, the timed-dispatch selection from a kernel
+trace, and the one-GPU contract."""
+import csv
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+import bench
+
+ROOT = Path(__file__).resolve().parent.parent
+COPY = "void pace_kv::(anonymous namespace)::page_copy_kernel<false, false>(pace_kv::(anonymous namespace)::CopyParams)"
+COPY_T = COPY.replace("<false, false>", "<false, true>")
+
+
+def write_csv(path, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    return str(path)
+
+
+def test_copy_kernel_names_follow_the_store_policy():
+    big = bench.TEMPORAL_STORE_MAX_BYTES + 1
+    assert bench.copy_kernel_names("buffer", big, 65536) == \
+        "page_copy_kernel<false, false> (pack and unpack, nontemporal stores)"
+    small = bench.copy_kernel_names("buffer", 64 << 20, 65536)
+    assert "page_copy_kernel<false, true> (pack, plain stores)" in small
+    assert "page_copy_kernel<false, false> (unpack" in small
+    assert bench.copy_kernel_names("fused", 64 << 20, 96).startswith("page_copy_kernel<true, false> (move")
+
+
+def test_summarize_pmc_scales_counters_by_the_calibration_copy(tmp_path):
+    gib_kib = float(1 << 20)
+    # FETCH_SIZE reads half of the true bytes, WRITE_SIZE all of them: the
+    # calibration copy of 1 GiB shows it and the factors undo it.
+    fetch = [{"Kernel_Name": COPY, "Counter_Name": "FETCH_SIZE", "Counter_Value": 1000.0},
+             {"Kernel_Name": COPY_T, "Counter_Name": "FETCH_SIZE", "Counter_Value": 1000.0},
+             {"Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": "FETCH_SIZE", "Counter_Value": gib_kib / 2},
+             {"Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": "FETCH_SIZE", "Counter_Value": 4.0}]
+    write = [{"Kernel_Name": COPY, "Counter_Name": "WRITE_SIZE", "Counter_Value": 2000.0},
+             {"Kernel_Name": COPY_T, "Counter_Name": "WRITE_SIZE", "Counter_Value": 2000.0},
+             {"Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": "WRITE_SIZE", "Counter_Value": gib_kib}]
+    d = bench.summarize_pmc(write_csv(tmp_path / "f.csv", fetch), write_csv(tmp_path / "w.csv", write), "config1")
+    assert d["fetch_scale"] == 2.0 and d["write_scale"] == 1.0     # the 4 KiB copy is not a calibration
+    assert d["fetch_bytes_per_launch"] == 2000 * 1024
+    assert d["write_bytes_per_launch"] == 2000 * 1024
+    assert d["traffic_bytes_per_launch"] == 4000 * 1024
+    assert d["fetch_dispatches"] == 2
+    assert d["kernel"] == "page_copy_kernel<false, false> and page_copy_kernel<false, true>"
+
+
+def test_summarize_pmc_needs_both_kinds_of_dispatch(tmp_path):
+    rows = [{"Kernel_Name": COPY, "Counter_Name": "FETCH_SIZE", "Counter_Value": 1.0}]
+    path = write_csv(tmp_path / "f.csv", rows)
+    with pytest.raises(SystemExit):
+        bench.summarize_pmc(path, path, "config2")
+
+
+def test_pmc_markdown_states_algorithmic_bytes_per_layer_chunk(tmp_path):
+    from paceserve_amd import workloads
+
+    w = workloads.config(5)
+    alg = 2 * 8 * w.n_pages * w.shape.page_bytes          # one launch = one 8-layer chunk
+    t = {"workload": "config5", "kernel": "page_copy_kernel<false, false>",
+         "fetch_kib_per_dispatch_raw": 1.0, "fetch_calibration_kib_raw": 2.0, "fetch_scale": 2.0,
+         "fetch_bytes_per_launch": alg // 2, "fetch_dispatches": 3, "write_kib_per_dispatch_raw": 1.0,
+         "write_calibration_kib_raw": 1.0, "write_scale": 1.0, "write_bytes_per_launch": alg // 2,
+         "write_dispatches": 3, "traffic_bytes_per_launch": alg}
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps(t))
+    md = bench.pmc_markdown(str(path))
+    assert f"Algorithmic bytes per launch: {alg} (8 layers x {w.n_pages} pages" in md
+    assert "= 1.00000 x algorithmic" in md
+    assert "--workload 5" in md
+
+
+def test_timed_dispatches_skip_warmup_and_later_passes(tmp_path):
+    # 2 warm-up steps and 3 timed steps of 2 launches, then 4 more launches
+    rows, t = [], 0
+    for i in range(2 * 2 + 3 * 2 + 4):
+        dur = 10 if 4 <= i < 10 else 99
+        rows.append({"Dispatch_Id": i + 1, "Kernel_Name": COPY, "Start_Timestamp": t,
+                     "End_Timestamp": t + dur})
+        t += dur + 1
+    rows.insert(3, {"Dispatch_Id": 100, "Kernel_Name": "other", "Start_Timestamp": 0, "End_Timestamp": 5})
+    path = write_csv(tmp_path / "k.csv", rows)
+    b = {"warmup": 2, "steps": 3, "roofline": {"launches_per_step": 2}}
+    durs, span = bench.timed_dispatches(path, b)
+    assert durs == [10] * 6
+    assert span == 6 * 10 + 5
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
