@@ -64,6 +64,29 @@ def build_library(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+C_CHECK_SRC = REPO_DIR / "tests" / "c_abi" / "pace_kv_check.c"
+C_CHECK_BIN = C_CHECK_SRC.with_suffix("")
+
+
+def build_c_check(verbose: bool = False) -> Path:
+    """Compiles the plain-C user of the ABI (tests/c_abi/pace_kv_check.c)
+    against the built library; the binary finds the library through its
+    rpath ($ORIGIN-relative) and the HIP runtime under ROCM_PATH."""
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    rel = os.path.relpath(PKG_DIR, C_CHECK_BIN.parent)
+    cmd = [os.environ.get("CC", "gcc"), "-std=c99", "-O2", "-Wall", "-Werror", "-D__HIP_PLATFORM_AMD__",
+           f"-I{rocm / 'include'}", f"-I{INCLUDE_DIR}", str(C_CHECK_SRC), "-o", str(C_CHECK_BIN),
+           f"-L{PKG_DIR}", "-lpace_kv", f"-L{rocm / 'lib'}", "-lamdhip64",
+           f"-Wl,-rpath,$ORIGIN/{rel}", f"-Wl,-rpath,{rocm / 'lib'}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError("C ABI check build failed:\n" + proc.stdout + proc.stderr)
+    return C_CHECK_BIN
+
+
 if __name__ == "__main__":
     path = build_library(verbose="-v" in sys.argv)
     print(path)
+    print(build_c_check(verbose="-v" in sys.argv))

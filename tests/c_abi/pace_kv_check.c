@@ -1,0 +1,139 @@
+/*
+ * A C (C99) user of libpace_kv.so through include/pace_kv.h alone: no Python,
+ * no torch.  Allocates two 3-layer pools with the HIP runtime, packs four
+ * pages of the source pool into a transfer buffer, unpacks them into other
+ * pages of the destination pool, and checks every byte on the host against a
+ * plain memcpy restatement.  Also checks that an argument error returns
+ * PACE_KV_EINVAL with a message.  Exit status 0 means every check passed.
+ *
+ * Build (the package build does this): gcc -std=c99 -D__HIP_PLATFORM_AMD__
+ *   -I/opt/rocm/include -Iinclude pace_kv_check.c -Lpaceserve_amd -lpace_kv
+ *   -L/opt/rocm/lib -lamdhip64
+ */
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "pace_kv.h"
+
+#define LAYERS 3
+#define POOL_PAGES 16
+#define PAGE_BYTES 4096
+#define N 4
+
+#define HIP_OK(expr)                                                      \
+  do {                                                                    \
+    hipError_t e_ = (expr);                                               \
+    if (e_ != hipSuccess) {                                               \
+      fprintf(stderr, "%s failed: %s\n", #expr, hipGetErrorString(e_));   \
+      return 2;                                                           \
+    }                                                                     \
+  } while (0)
+
+static unsigned char pattern(int pool, int layer, int page, int offset) {
+  return (unsigned char)(pool * 101 + layer * 37 + page * 13 + offset * 7 + (offset >> 8));
+}
+
+int main(void) {
+  const size_t pool_bytes = (size_t)POOL_PAGES * PAGE_BYTES;
+  const int32_t src_ids[N] = {5, 0, 11, 3};
+  const int32_t dst_ids[N] = {2, 9, 14, 7};
+  unsigned char* host_src[LAYERS];
+  unsigned char* host_dst[LAYERS];
+  void* src_layers[LAYERS];
+  void* dst_layers[LAYERS];
+  void *buf, *ids_src, *ids_dst;
+  unsigned char* host_buf = malloc((size_t)LAYERS * N * PAGE_BYTES);
+  unsigned char* got = malloc(pool_bytes);
+  int l, j, p, failures = 0;
+
+  if (host_buf == NULL || got == NULL) return 2;
+  HIP_OK(hipSetDevice(0));
+  for (l = 0; l < LAYERS; ++l) {
+    host_src[l] = malloc(pool_bytes);
+    host_dst[l] = malloc(pool_bytes);
+    if (host_src[l] == NULL || host_dst[l] == NULL) return 2;
+    for (p = 0; p < POOL_PAGES; ++p)
+      for (j = 0; j < PAGE_BYTES; ++j) {
+        host_src[l][(size_t)p * PAGE_BYTES + j] = pattern(0, l, p, j);
+        host_dst[l][(size_t)p * PAGE_BYTES + j] = pattern(1, l, p, j);
+      }
+    HIP_OK(hipMalloc(&src_layers[l], pool_bytes));
+    HIP_OK(hipMalloc(&dst_layers[l], pool_bytes));
+    HIP_OK(hipMemcpy(src_layers[l], host_src[l], pool_bytes, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dst_layers[l], host_dst[l], pool_bytes, hipMemcpyHostToDevice));
+  }
+  HIP_OK(hipMalloc(&buf, (size_t)LAYERS * N * PAGE_BYTES));
+  HIP_OK(hipMalloc(&ids_src, sizeof(src_ids)));
+  HIP_OK(hipMalloc(&ids_dst, sizeof(dst_ids)));
+  HIP_OK(hipMemcpy(ids_src, src_ids, sizeof(src_ids), hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(ids_dst, dst_ids, sizeof(dst_ids), hipMemcpyHostToDevice));
+
+  if (pace_kv_abi_version() != PACE_KV_ABI_VERSION) {
+    fprintf(stderr, "ABI version %d, header %d\n", pace_kv_abi_version(), PACE_KV_ABI_VERSION);
+    return 1;
+  }
+  /* NULL stream: the device's null stream. */
+  int rc = pace_kv_pack((const void* const*)src_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_src, N,
+                        PAGE_BYTES, buf, (int64_t)N * PAGE_BYTES, NULL, NULL);
+  if (rc == PACE_KV_OK)
+    rc = pace_kv_unpack(buf, (int64_t)N * PAGE_BYTES, dst_layers, LAYERS, POOL_PAGES,
+                        (const int32_t*)ids_dst, N, PAGE_BYTES, NULL, NULL);
+  if (rc != PACE_KV_OK) {
+    fprintf(stderr, "pack/unpack status %d: %s\n", rc, pace_kv_last_error());
+    return 1;
+  }
+  HIP_OK(hipDeviceSynchronize());
+
+  /* transfer buffer: buf[l][j] = src[l][src_ids[j]] */
+  HIP_OK(hipMemcpy(host_buf, buf, (size_t)LAYERS * N * PAGE_BYTES, hipMemcpyDeviceToHost));
+  for (l = 0; l < LAYERS; ++l)
+    for (j = 0; j < N; ++j)
+      if (memcmp(host_buf + ((size_t)l * N + j) * PAGE_BYTES,
+                 host_src[l] + (size_t)src_ids[j] * PAGE_BYTES, PAGE_BYTES) != 0) {
+        fprintf(stderr, "buffer layer %d page %d differs\n", l, j);
+        ++failures;
+      }
+  /* destination: named pages receive the source pages, the rest is unchanged */
+  for (l = 0; l < LAYERS; ++l) {
+    for (j = 0; j < N; ++j)
+      memcpy(host_dst[l] + (size_t)dst_ids[j] * PAGE_BYTES, host_src[l] + (size_t)src_ids[j] * PAGE_BYTES,
+             PAGE_BYTES);
+    HIP_OK(hipMemcpy(got, dst_layers[l], pool_bytes, hipMemcpyDeviceToHost));
+    if (memcmp(got, host_dst[l], pool_bytes) != 0) {
+      fprintf(stderr, "destination layer %d differs\n", l);
+      ++failures;
+    }
+    HIP_OK(hipMemcpy(got, src_layers[l], pool_bytes, hipMemcpyDeviceToHost));
+    if (memcmp(got, host_src[l], pool_bytes) != 0) {
+      fprintf(stderr, "source layer %d was written\n", l);
+      ++failures;
+    }
+  }
+
+  /* an argument error is caught on the host, before any launch */
+  rc = pace_kv_pack((const void* const*)src_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_src, N, 100,
+                    buf, (int64_t)N * PAGE_BYTES, NULL, NULL);
+  if (rc != PACE_KV_EINVAL || strlen(pace_kv_last_error()) == 0) {
+    fprintf(stderr, "page_bytes 100: status %d, message '%s'\n", rc, pace_kv_last_error());
+    ++failures;
+  }
+
+  for (l = 0; l < LAYERS; ++l) {
+    HIP_OK(hipFree(src_layers[l]));
+    HIP_OK(hipFree(dst_layers[l]));
+    free(host_src[l]);
+    free(host_dst[l]);
+  }
+  HIP_OK(hipFree(buf));
+  HIP_OK(hipFree(ids_src));
+  HIP_OK(hipFree(ids_dst));
+  free(host_buf);
+  free(got);
+  if (failures) return 1;
+  printf("pace_kv C ABI check passed: %d layers x %d pages of %d B packed and unpacked\n", LAYERS, N,
+         PAGE_BYTES);
+  return 0;
+}

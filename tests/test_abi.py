@@ -92,3 +92,17 @@ def test_check_raises_with_message(lib):
     rc = lib.pace_kv_pack(_layers(2), -1, 10, 0x100, 4, 65536, 0x1000, 4 * 65536, None, None)
     with pytest.raises(_native.PaceKVError, match="num_layers"):
         _native.check(rc)
+
+
+@pytest.mark.parametrize("compiler,flags", [("gcc", ["-x", "c", "-std=c99"]), ("g++", ["-x", "c++", "-std=c++11"])])
+def test_header_is_self_contained_c_and_cpp(tmp_path, compiler, flags):
+    import shutil
+    import subprocess
+
+    if shutil.which(compiler) is None:
+        pytest.skip(f"{compiler} not installed")
+    src = tmp_path / "use_header.c"
+    src.write_text('#include "pace_kv.h"\nint f(void) { return pace_kv_abi_version() + PACE_KV_OK; }\n')
+    r = subprocess.run([compiler, *flags, "-Wall", "-Wextra", "-Werror", "-pedantic", f"-I{HEADER.parent}",
+                        "-fsyntax-only", str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

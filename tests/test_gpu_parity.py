@@ -247,3 +247,50 @@ def test_stager_rejects_oversized_chunks(gpu):
     with ops.Stager(65536 * 3, 2) as st:         # one layer of 4 pages needs 4 * 65536
         with pytest.raises(_native.PaceKVError, match="slot holds"):
             st.pack_to_host(src, [0, 1, 2, 3], host, 1)
+
+
+def test_concurrent_host_threads_on_their_own_streams(gpu):
+    # The reference inserts from several Ray threads at once; the entry points
+    # hold no global state, so threads driving their own streams interleave
+    # freely.  Each thread moves its own disjoint set of pages.
+    import threading
+
+    L, pages, shape, threads, rounds = 4, 256, (2, 16, 8, 128), 4, 25
+    src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 21)
+    dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 22)
+    src_pool, dst_pool = ops.PagedPool(src), ops.PagedPool(dst)
+    perm = torch.randperm(pages, generator=torch.Generator().manual_seed(23))
+    share = pages // threads
+    sets = [(perm[t * share:(t + 1) * share].tolist(), perm.flip(0)[t * share:(t + 1) * share].tolist())
+            for t in range(threads)]
+    errors = []
+
+    def worker(t):
+        try:
+            s_ids, d_ids = sets[t]
+            stream = torch.cuda.Stream(gpu)
+            with torch.cuda.stream(stream):
+                s_dev = torch.tensor(s_ids, dtype=torch.int32, device=gpu)
+                d_dev = torch.tensor(d_ids, dtype=torch.int32, device=gpu)
+                for r in range(rounds):
+                    if r % 2:
+                        ops.move(src_pool, s_dev, dst_pool, d_dev)
+                    else:
+                        buf = ops.pack(src_pool, s_dev)
+                        ops.unpack(buf, dst_pool, d_dev)
+            stream.synchronize()
+        except Exception as e:          # reported by the main thread
+            errors.append((t, repr(e)))
+
+    ts = [threading.Thread(target=worker, args=(t,)) for t in range(threads)]
+    for th in ts:
+        th.start()
+    for th in ts:
+        th.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for s_ids, d_ids in sets:
+        si = torch.tensor(s_ids, device=gpu)
+        di = torch.tensor(d_ids, device=gpu)
+        for l in range(L):
+            assert same(dst[l].index_select(0, di), src[l].index_select(0, si))

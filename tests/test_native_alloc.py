@@ -97,3 +97,61 @@ def test_block_space_manager_native_backend():
     bm.free(s)
     assert bm.get_num_free_gpu_blocks() == 10
     assert bm.gpu_allocator.free_blocks == [0, 1, 2, 3, 4, 5, 6, 9, 8, 7]
+
+
+def test_concurrent_threads_never_share_a_page():
+    # ctypes releases the GIL, so these calls run concurrently in the
+    # library; its mutex must hand each page to one holder at a time.
+    import threading
+
+    pages, threads, rounds = 257, 8, 1500
+    a = NativeBlockAllocator(16, pages)
+    owner = np.full(pages, -1, dtype=np.int64)
+    errors = []
+
+    def worker(tid):
+        rng = np.random.default_rng(tid)
+        for _ in range(rounds):
+            try:
+                got = a.allocate_many(int(rng.integers(1, 9)))
+            except ValueError:          # momentarily out of pages: try again
+                continue
+            for p in got:
+                if owner[p] != -1:
+                    errors.append((tid, p, int(owner[p])))
+                owner[p] = tid
+            for p in got:
+                owner[p] = -1
+            a.free_many(got)
+
+    ts = [threading.Thread(target=worker, args=(t,)) for t in range(threads)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors, errors[:5]
+    assert a.get_num_free_blocks() == pages
+    assert sorted(a.allocate_many(pages)) == list(range(pages))
+
+
+def test_last_error_is_per_thread():
+    import threading
+
+    lib = _native.load()
+    a = NativeBlockAllocator(16, 4)
+    msgs = {}
+    barrier = threading.Barrier(2)
+
+    def fail_with(tid, bad):
+        ids = np.array([bad], dtype=np.int32)
+        rc = lib.pace_kv_allocator_free(a.handle, ids.ctypes.data, 1)
+        barrier.wait()                 # both threads have failed before either reads
+        msgs[tid] = (rc, lib.pace_kv_last_error().decode())
+
+    ts = [threading.Thread(target=fail_with, args=(0, 4)), threading.Thread(target=fail_with, args=(1, -3))]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert msgs[0][0] == msgs[1][0] == _native.PACE_KV_ERANGE
+    assert "page id 4 " in msgs[0][1] and "page id -3 " in msgs[1][1]
