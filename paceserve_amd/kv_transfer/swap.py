@@ -26,6 +26,12 @@ class SwapSpace:
         self.host = ops.HostPagePool.like(self.dev, num_host_pages)
         self.host_allocator = NativeBlockAllocator(self.dev.page_shape[1], num_host_pages)
         self.tables: Dict[str, List[int]] = {}   # seq_id -> host pages
+        # seq_id -> event recorded after its swap-out: its swap-in, on any
+        # stream, reads the host pages only after they are written.
+        self._swapped_out: Dict[str, torch.cuda.Event] = {}
+        # Recorded after each swap-in: host pages it freed are reused only by
+        # work ordered after it, whichever stream that work runs on.
+        self._swapped_in: Optional[torch.cuda.Event] = None
 
     def num_free_host_pages(self) -> int:
         return self.host_allocator.get_num_free_blocks()
@@ -38,24 +44,34 @@ class SwapSpace:
         ids = normalize_page_ids(dev_table, self.dev.num_pages)
         host_table = self.host_allocator.allocate_many(len(ids))
         try:
+            if self._swapped_in is not None:
+                torch.cuda.current_stream(self.dev.device).wait_event(self._swapped_in)
             ops.swap_out(self.dev, ids, self.host, host_table)
         except Exception:
             self.host_allocator.free_many(reversed(host_table))
             raise
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.dev.device))
+        self._swapped_out[seq_id] = ev
         self.tables[seq_id] = host_table
         return host_table
 
     def swap_in(self, seq_id: str, dev_table: List[int]) -> None:
         """Copies the request's host pages into dev_table (allocated by the
-        caller) and returns the host pages to the host allocator.  The copy is
-        ordered before later work on the current stream, which is where a
-        reuse of those host pages would be enqueued."""
+        caller) and returns the host pages to the host allocator.  The copy
+        waits for the request's swap_out, and a later swap_out, on any
+        stream, waits for this copy before it writes host pages."""
         host_table = self.tables.pop(seq_id)
         ids = normalize_page_ids(dev_table, self.dev.num_pages)
         if len(ids) != len(host_table):
             self.tables[seq_id] = host_table
             raise ValueError(f"{len(ids)} device pages for {len(host_table)} swapped pages")
+        stream = torch.cuda.current_stream(self.dev.device)
+        stream.wait_event(self._swapped_out.pop(seq_id))
         ops.swap_in(self.host, host_table, self.dev, ids)
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        self._swapped_in = ev
         self.host_allocator.free_many(host_table)
 
     def holds(self, seq_id: str) -> bool:

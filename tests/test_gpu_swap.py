@@ -103,6 +103,37 @@ def test_swap_space_preemption_round_trip(gpu):
         space.swap_in("req-1", new_table)
 
 
+def test_swap_space_orders_work_across_streams(gpu):
+    # Swap out on one stream and in on another with no host synchronisation:
+    # the swap-in waits for the swap-out that wrote its host pages, and a
+    # later swap-out reusing those host pages waits for the swap-in.
+    dev = dev_pool(gpu, 1280, 9)
+    alloc = NativeBlockAllocator(16, 1280)
+    space = SwapSpace(dev, 400)
+    ids = lambda t: torch.tensor(t, device=gpu)           # noqa: E731
+    t1, t2 = alloc.allocate_many(400), alloc.allocate_many(400)
+    saved1 = [words(t[ids(t1)]).clone() for t in dev.layers]
+    saved2 = [words(t[ids(t2)]).clone() for t in dev.layers]
+    new1 = alloc.allocate_many(400)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)
+    with torch.cuda.stream(a):
+        space.swap_out("r1", t1)
+    with torch.cuda.stream(b):
+        space.swap_in("r1", new1)
+    with torch.cuda.stream(a):
+        space.swap_out("r2", t2)           # reuses r1's host pages
+    torch.cuda.synchronize()
+    for l in range(SHAPE.num_layers):
+        assert torch.equal(words(dev.layers[l][ids(new1)]), saved1[l])
+    alloc.free_many(new1)
+    new2 = alloc.allocate_many(400)
+    space.swap_in("r2", new2)
+    torch.cuda.synchronize()
+    for l in range(SHAPE.num_layers):
+        assert torch.equal(words(dev.layers[l][ids(new2)]), saved2[l])
+
+
 def test_swap_4k_request(gpu):
     w = workloads.config("promote4k")
     dev = ops.PagedPool(workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, gpu))
