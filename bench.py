@@ -294,7 +294,7 @@ def run_staging(w, dev, src, dst, s_ids, d_ids, reps: int = 3):
 
     L, n, pb = w.shape.num_layers, s_ids.numel(), w.shape.page_bytes
     layer_bytes = n * pb
-    k = w.layers_per_chunk or kv_utils.chunk_layers(L, layer_bytes)
+    k = w.layers_per_chunk or kv_utils.roundtrip_chunk_layers(L, layer_bytes)
     chunk = k * layer_bytes
     chunks = -(-L // k)
     # host ring of up to 4 chunk regions (a full copy for short payloads)

@@ -169,8 +169,8 @@ class KVMigrator:
                 ops.pack(self.src, src_ids, buf[: le - lb], layer_begin=lb, layer_end=le)
                 ops.unpack(buf[: le - lb], self.dst, dst_ids, layer_begin=lb, layer_end=le)
         elif mode == "pinned":
-            from .kv_utils import chunk_layers
-            k = layers_per_chunk or chunk_layers(L, n * self.src.page_bytes)
+            from .kv_utils import roundtrip_chunk_layers
+            k = layers_per_chunk or roundtrip_chunk_layers(L, n * self.src.page_bytes)
             slot = k * n * self.src.page_bytes
             if self.stager is None or self.stager.slot_bytes < slot:
                 if self.stager is not None:

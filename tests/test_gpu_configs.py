@@ -112,7 +112,7 @@ def test_workload_pinned_roundtrip(gpu, c):
     before = sums_before(src, dst, s_ids, d_ids)
     from paceserve_amd.kv_transfer import kv_utils
     n = plan.n_pages
-    k = w.layers_per_chunk or kv_utils.chunk_layers(w.shape.num_layers, n * w.shape.page_bytes)
+    k = w.layers_per_chunk or kv_utils.roundtrip_chunk_layers(w.shape.num_layers, n * w.shape.page_bytes)
     chunk = k * n * w.shape.page_bytes
     host = torch.empty(min(w.payload_bytes, 3 * chunk), dtype=torch.uint8, pin_memory=True)
     with ops.Stager(chunk, 3, gpu) as st:

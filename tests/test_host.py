@@ -7,7 +7,8 @@ from oracle import kv_oracle as orc
 from paceserve_amd.core.block_manager import BlockAllocator, BlockSpaceManager, remap_dst_table
 from paceserve_amd.core.kv_cache_obj import KVobj
 from paceserve_amd.core.sequence import Sequence
-from paceserve_amd.kv_transfer.kv_utils import chunk_layers, dedup_keep_last, normalize_page_ids
+from paceserve_amd.kv_transfer.kv_utils import (chunk_layers, dedup_keep_last, normalize_page_ids,
+                                                roundtrip_chunk_layers)
 from paceserve_amd.kv_transfer.migrate import flatten_tables, plan_batch
 from paceserve_amd.kv_transfer.worker import KVStatus, KVWorker, WorkerSequenceManager
 
@@ -127,10 +128,28 @@ def test_flatten_tables_matches_per_request_normalization():
 
 
 def test_chunk_layers():
-    assert chunk_layers(32, 64 << 20) == 1
-    assert chunk_layers(32, 2 << 20) == 8        # at least 4 chunks
-    assert chunk_layers(32, 512 << 20) == 1
-    assert chunk_layers(1, 1) == 1
+    MiB = 1 << 20
+    assert chunk_layers(32, 64 * MiB) == 1
+    assert chunk_layers(32, 16 * MiB) == 4       # 64 MiB chunks
+    assert chunk_layers(32, 2 * MiB) == 32       # one 64 MiB chunk
+    assert chunk_layers(32, 3 * MiB) == 22       # the fewest layers reaching 64 MiB
+    assert chunk_layers(32, 512 * MiB) == 1
+    assert chunk_layers(1, 1) == 1 and chunk_layers(5, 0) == 5
+
+
+def test_roundtrip_chunk_layers_avoid_many_small_chunks():
+    MiB = 1 << 20
+    # 32 layers of Llama-3-8B pages: requests of 512 .. 8192 tokens
+    got = {tok: roundtrip_chunk_layers(32, tok // 16 * 64 * 1024) for tok in (512, 1024, 2048, 4096, 8192)}
+    assert got == {512: 8, 1024: 4, 2048: 4, 4096: 2, 8192: 2}
+    assert roundtrip_chunk_layers(32, 128 * MiB) == 1     # large chunks: any count
+    assert roundtrip_chunk_layers(32, 1 * MiB) == 16      # two 16 MiB chunks
+    assert roundtrip_chunk_layers(32, MiB // 4) == 32     # 8 MiB in all: one chunk
+    assert roundtrip_chunk_layers(80, 16 * MiB) == 5      # 80-layer cache: 16 chunks of 80 MiB
+    for layers in (1, 7, 32, 80):
+        for mib in (1, 3, 8, 40, 300):
+            k = roundtrip_chunk_layers(layers, mib * MiB)
+            assert 1 <= k <= layers
 
 
 class _FakeHelper:
