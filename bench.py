@@ -261,28 +261,30 @@ def run_ceiling(w, dev, src, dst, n: int, reps: int = 10) -> dict:
     return {"identity_ids_gbs": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def link_settle(dev, target_gbs: float = 45.0, max_wait_s: float = 15.0) -> dict:
-    """Waits until a 64 MiB pinned device-to-host copy runs at target_gbs or
-    more (other DMA work, such as the driver scrubbing freed device memory,
-    shares the engines), for at most max_wait_s; returns what it saw."""
+def link_settle(dev, target_gbs: float = 45.0, max_wait_s: float = 30.0, streak: int = 3) -> dict:
+    """Waits until `streak` consecutive 64 MiB pinned device-to-host copies,
+    0.2 s apart, each run at target_gbs or more (other DMA work, such as the
+    driver scrubbing device memory that an earlier process freed, shares the
+    engines in bursts), for at most max_wait_s; returns what it saw."""
     import torch
 
     nbytes = 64 << 20
     a = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
     h = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
     t_start = time.perf_counter()
-    rate = 0.0
+    rate, good = 0.0, 0
     while True:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         h.copy_(a, non_blocking=True)
         torch.cuda.synchronize()
         rate = nbytes / (time.perf_counter() - t0) / 1e9
+        good = good + 1 if rate >= target_gbs else 0
         waited = time.perf_counter() - t_start
-        if rate >= target_gbs or waited >= max_wait_s:
+        if good >= streak or waited >= max_wait_s:
             break
-        time.sleep(0.5)
-    return {"d2h_gbs": round(rate, 1), "waited_s": round(waited, 2)}
+        time.sleep(0.2)
+    return {"d2h_gbs": round(rate, 1), "waited_s": round(waited, 2), "settled": good >= streak}
 
 
 def run_staging(w, dev, src, dst, s_ids, d_ids, reps: int = 3):

@@ -4,13 +4,17 @@
 // (device->host, host->device), at <= ~64 GB/s per direction, i.e. two orders
 // of magnitude slower than the on-device pack/unpack.  The pipeline therefore
 // aims to keep both DMA directions busy at once and to hide pack/unpack under
-// them: layers are processed in chunks, and with three streams
-//   caller stream : pack(c) ........ unpack(c-2)
-//   D2H stream    :        D2H(c)
-//   H2D stream    :               H2D(c-1)
+// them: layers are processed in chunks, and the round trip uses four streams
+//   caller stream : pack(c+1)
+//   D2H stream    : D2H(c)
+//   H2D stream    : H2D(c-1)
+//   unpack stream : unpack(c-2)
 // chunk c's device-to-host copy overlaps chunk c-1's host-to-device copy (the
 // two directions use separate DMA engines) and the kernels of neighbouring
-// chunks.  Events carry every dependency; nothing blocks the host.
+// chunks.  Unpacks have a stream of their own so that waiting for a chunk's
+// host-to-device copy never holds back the packs that feed the other
+// direction (measured: 1.5% faster than unpacking on the caller stream).
+// Events carry every dependency; nothing blocks the host.
 //
 // Device slots are reused round-robin; before a slot is overwritten, the
 // stream that writes it waits for the event recorded after the last read of
@@ -32,8 +36,10 @@ struct pace_kv_stager {
   char* in_ring = nullptr;   // num_slots device slots written by H2D, read by unpack
   hipStream_t d2h = nullptr;
   hipStream_t h2d = nullptr;
+  hipStream_t unpack = nullptr;  // round trip: unpacks of the host chunks
   hipEvent_t start = nullptr;
   hipEvent_t d2h_done = nullptr;
+  hipEvent_t unpack_done = nullptr;
   std::vector<hipEvent_t> packed;    // out slot s filled (caller stream)
   std::vector<hipEvent_t> out_free;  // out slot s drained by D2H (D2H stream)
   std::vector<hipEvent_t> in_ready;  // in slot s filled by H2D (H2D stream)
@@ -64,8 +70,10 @@ void release(pace_kv_stager* s) {
   if (s->in_ring) (void)hipFree(s->in_ring);
   if (s->d2h) (void)hipStreamDestroy(s->d2h);
   if (s->h2d) (void)hipStreamDestroy(s->h2d);
+  if (s->unpack) (void)hipStreamDestroy(s->unpack);
   if (s->start) (void)hipEventDestroy(s->start);
   if (s->d2h_done) (void)hipEventDestroy(s->d2h_done);
+  if (s->unpack_done) (void)hipEventDestroy(s->unpack_done);
   destroy_events(s->packed);
   destroy_events(s->out_free);
   destroy_events(s->in_ready);
@@ -154,8 +162,10 @@ int pace_kv_stager_create(int64_t slot_bytes, int num_slots, pace_kv_stager** ou
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&s->in_ring), slot_bytes * num_slots);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->d2h, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->h2d, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->unpack, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&s->start, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&s->d2h_done, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&s->unpack_done, hipEventDisableTiming);
   if (e == hipSuccess) e = make_events(s->packed, num_slots);
   if (e == hipSuccess) e = make_events(s->out_free, num_slots);
   if (e == hipSuccess) e = make_events(s->in_ready, num_slots);
@@ -174,10 +184,12 @@ int pace_kv_stager_destroy(pace_kv_stager* s) {
   // Work enqueued through the stager may still use its slots and streams.
   hipError_t e1 = hipStreamSynchronize(s->d2h);
   hipError_t e2 = hipStreamSynchronize(s->h2d);
+  hipError_t e3 = hipStreamSynchronize(s->unpack);
   for (hipEvent_t e : s->in_free) (void)hipEventSynchronize(e);
   release(s);
   if (e1 != hipSuccess) return hip_status(e1, "stager_destroy (D2H stream)");
-  return hip_status(e2, "stager_destroy (H2D stream)");
+  if (e2 != hipSuccess) return hip_status(e2, "stager_destroy (H2D stream)");
+  return hip_status(e3, "stager_destroy (unpack stream)");
 }
 
 int pace_kv_pack_to_host(pace_kv_stager* s, const void* const* src_layers, int num_layers,
@@ -256,20 +268,14 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
   PACE_HIP(make_events(s->host_free, regions), "create host events");
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   char* host = static_cast<char*>(host_buf);
+  // The H2D copies and the unpacks come after the caller's earlier work.
   PACE_HIP(hipEventRecord(s->start, stream), "record start");
   PACE_HIP(hipStreamWaitEvent(s->h2d, s->start, 0), "wait start");
-  // unpack(c) is issued on the caller stream after pack(c + kLag), so that the
-  // stream's wait for H2D(c) does not hold back the packs that feed the D2H
-  // queue.
-  const int kLag = 2;
-  int next_unpack = 0;
-  auto issue_unpack = [&](int c) -> int {
-    const int slot = c % s->num_slots;
-    PACE_HIP(hipStreamWaitEvent(stream, s->in_ready[slot], 0), "wait in_ready");
-    PACE_KV_TRY(unpack_chunk(s, p, c, dst_layers, dst_pool_pages, dst_ids, err_count, stream));
-    PACE_HIP(hipEventRecord(s->in_free[slot], stream), "record in_free");
-    return PACE_KV_OK;
-  };
+  PACE_HIP(hipStreamWaitEvent(s->unpack, s->start, 0), "wait start");
+  // Every wait below names an event whose last record was enqueued in an
+  // earlier iteration (or an earlier call), so it orders against the right
+  // chunk: slot reuse waits for chunk c - num_slots, host region reuse for
+  // chunk c - regions.
   for (int c = 0; c < chunks; ++c) {
     const int slot = c % s->num_slots;
     const int r = c % regions;
@@ -285,10 +291,6 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
              "D2H copy");
     PACE_HIP(hipEventRecord(s->out_free[slot], s->d2h), "record out_free");
     PACE_HIP(hipEventRecord(s->host_full[r], s->d2h), "record host_full");
-    // unpack(c - kLag) last reads in slot (c - kLag) % num_slots; it must be
-    // enqueued before H2D(c) waits on in_free of slot c % num_slots, which is
-    // the same slot when num_slots == kLag.
-    if (c - kLag >= next_unpack) PACE_KV_TRY(issue_unpack(next_unpack++));
     PACE_HIP(hipStreamWaitEvent(s->h2d, s->host_full[r], 0), "wait host_full");
     PACE_HIP(hipStreamWaitEvent(s->h2d, s->in_free[slot], 0), "wait in slot");
     PACE_HIP(hipMemcpyAsync(s->in_ring + slot * s->slot_bytes, region, bytes,
@@ -296,8 +298,13 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
              "H2D copy");
     PACE_HIP(hipEventRecord(s->in_ready[slot], s->h2d), "record in_ready");
     PACE_HIP(hipEventRecord(s->host_free[r], s->h2d), "record host_free");
+    PACE_HIP(hipStreamWaitEvent(s->unpack, s->in_ready[slot], 0), "wait in_ready");
+    PACE_KV_TRY(unpack_chunk(s, p, c, dst_layers, dst_pool_pages, dst_ids, err_count, s->unpack));
+    PACE_HIP(hipEventRecord(s->in_free[slot], s->unpack), "record in_free");
   }
-  while (next_unpack < chunks) PACE_KV_TRY(issue_unpack(next_unpack++));
+  // The caller's later work sees every destination page written.
+  PACE_HIP(hipEventRecord(s->unpack_done, s->unpack), "record unpack_done");
+  PACE_HIP(hipStreamWaitEvent(stream, s->unpack_done, 0), "join unpacks");
   return PACE_KV_OK;
 }
 
