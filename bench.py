@@ -1,9 +1,9 @@
 """Benchmark of the KV-cache migration hot path on one MI355X.
 
-Default workload (N=1): config 2 - 16 requests with lognormal(median 1024,
-sigma 1.0) token counts clipped to [128, 8192], Llama-3-8B KV shape (32
-layers, 8 KV heads, head_dim 128, page 16), bf16, 16384-page source and
-destination pools, fragmented source free list.  One step = pack every
+Default workload (N=1): llama3-8b-16req-bf16 - 16 requests with
+lognormal(median 1024, sigma 1.0) token counts clipped to [128, 8192],
+Llama-3-8B KV shape (32 layers, 8 KV heads, head_dim 128, page 16), bf16,
+16384-page source and destination pools, fragmented source free list.  One step = pack every
 request's pages from all layers into the contiguous transfer buffer, then
 unpack the buffer into the destination pages (the reference's
 get_kv_cache + insert_kv_cache, moved on-device).
@@ -18,8 +18,9 @@ pack + unpack, to completion) and the reference's CPU path (torch
 index_select / index_copy_ on host tensors) timed on a bounded sample on this
 host's cores.
 
-Usage: python bench.py [--steps K] [--warmup W] [--workload 1..5]
+Usage: python bench.py [--steps K] [--warmup W] [--workload NAME]
        [--no-cpu] [--no-promote] [--verify]
+(NAME: one of paceserve_amd.workloads.NAMES; see that module)
 """
 from __future__ import annotations
 
@@ -47,11 +48,13 @@ def log(msg: str) -> None:
 
 
 def parse_args():
+    from paceserve_amd import workloads
+
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--workload", default=workloads.DEFAULT, choices=workloads.NAMES)
     ap.add_argument("--mode", default="buffer", choices=["buffer", "fused"],
                     help="buffer: pack + unpack (the metric); fused: pool-to-pool move")
     ap.add_argument("--no-cpu", action="store_true")
@@ -352,7 +355,7 @@ def run_promote(dev, steps=100, warmup=10):
     from paceserve_amd.core.block_manager import BlockAllocator, NativeBlockAllocator
     from paceserve_amd.kv_transfer import migrate
 
-    w = workloads.config("promote4k")
+    w = workloads.get(workloads.PROMOTE)
     src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev)
     dst = workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev)
     host = torch.empty(w.payload_bytes, dtype=torch.uint8, pin_memory=True)
@@ -380,7 +383,7 @@ def run_promote(dev, steps=100, warmup=10):
         lat.sort()
         out[mode] = {"p50_us": round(statistics.median(lat), 1),
                      "p90_us": round(lat[int(0.9 * (len(lat) - 1))], 1), "runs": len(lat)}
-        log(f"promote4k {mode}: p50 {out[mode]['p50_us']} us")
+        log(f"promote 4096 tok {mode}: p50 {out[mode]['p50_us']} us")
     # swap of the same request into a pinned host page pool and back
     from paceserve_amd.kv_transfer import ops
     dpool = ops.PagedPool(src)
@@ -399,7 +402,7 @@ def run_promote(dev, steps=100, warmup=10):
         lat.sort()
         out[name] = {"p50_us": round(statistics.median(lat), 1),
                      "gbs": round(w.payload_bytes / (statistics.median(lat) * 1e-6) / 1e9, 2), "runs": len(lat)}
-        log(f"promote4k {name}: p50 {out[name]['p50_us']} us ({out[name]['gbs']} GB/s)")
+        log(f"promote 4096 tok {name}: p50 {out[name]['p50_us']} us ({out[name]['gbs']} GB/s)")
     out["payload_bytes"] = w.payload_bytes
     # the metric's promote latency: allocation + remap + id upload + pack +
     # unpack, through the single library call
@@ -635,12 +638,11 @@ def pmc_markdown(traffic_json: str) -> str:
     wl = t["workload"]
     from paceserve_amd import workloads
 
-    c = wl.replace("config", "")
-    w = workloads.config(int(c))
+    w = workloads.get(wl)
     # one launch reads and writes its layer chunk's pages once
     chunk = min(w.device_layers_per_chunk or w.shape.num_layers, w.shape.num_layers)
     alg = 2 * chunk * w.n_pages * w.shape.page_bytes
-    run = f"python3 bench.py --workload {c} --no-cpu --no-promote --no-staging --steps 3 --warmup 1 --calibrate"
+    run = f"python3 bench.py --workload {wl} --no-cpu --no-promote --no-staging --steps 3 --warmup 1 --calibrate"
     cmds = [
         "export TMPDIR=/tmp",
         f"timeout -s KILL 300 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch_{wl} -o f -- {run}",
@@ -708,7 +710,7 @@ def main():
 
     _native.load()
     dev = torch.device("cuda", 0)
-    w = workloads.config(args.workload)
+    w = workloads.get(args.workload)
     log(f"workload {w.name}: {w.description}")
     src, dst, plan, s_ids, d_ids = device_setup(w, dev)
     res = run_device(args, w, dev, src, dst, plan, s_ids, d_ids)

@@ -4,26 +4,31 @@ Each workload fixes the cache shape, the source/destination pool sizes, the
 request lengths and how the source pool's free list is fragmented, so that the
 benchmark and the tests build identical source block tables and pages:
 
-  config 1  Llama-3-8B KV (32 layers, 8 KV heads, head_dim 128, page 16), fp16:
-            one 512-token request (32 pages) at seeded random pages of a
-            2048-page pool, values N(0,1).
-  config 2  same shape, bf16: 16 requests, lengths lognormal(median 1024,
-            sigma 1.0) clipped to [128, 8192]; 16384-page pools; the source
-            free list is a seeded permutation; separate fresh destination pool.
-  config 3  Llama-2-7B KV (32 KV heads), fp16: 8 requests of 4095 tokens
-            (256 pages each, last page 15/16 full); 4096-page pools, permuted;
-            migrated through pinned host memory, one layer per chunk.
-  config 4  Llama-3-8B KV, bf16, values uniform[-4, 4]: one 32768-token
-            request filling a 2048-page pool in permuted order; on-device and
-            pinned-host variants.
-  config 5  Llama-3-70B KV (80 layers, 8 KV heads), bf16: 256 requests of
-            U{64..2048} tokens; 20480-page pools; a seeded permutation of the
-            source pool dealt to requests round-robin one page at a time;
-            moved in 8-layer chunks.
-  promote4k Llama-3-8B KV, bf16: one 4096-token request (256 pages) in a
-            2048-page pool (the promote-latency workload).
-
-Seed 1000 + c for config c (1100 for promote4k).
+  llama3-8b-512tok-fp16      Llama-3-8B KV (32 layers, 8 KV heads, head_dim
+                             128, page 16), fp16: one 512-token request (32
+                             pages) at seeded random pages of a 2048-page pool,
+                             values N(0,1).  Seed 1001.
+  llama3-8b-16req-bf16       same shape, bf16: 16 requests, lengths
+                             lognormal(median 1024, sigma 1.0) clipped to
+                             [128, 8192]; 16384-page pools; the source free
+                             list is a seeded permutation; separate fresh
+                             destination pool.  Seed 1002.
+  llama2-7b-8x4095tok-fp16   Llama-2-7B KV (32 KV heads), fp16: 8 requests of
+                             4095 tokens (256 pages each, last page 15/16
+                             full); 4096-page pools, permuted; migrated through
+                             pinned host memory, one layer per chunk.  Seed 1003.
+  llama3-8b-32768tok-bf16    Llama-3-8B KV, bf16, values uniform[-4, 4]: one
+                             32768-token request filling a 2048-page pool in
+                             permuted order; on-device and pinned-host
+                             variants.  Seed 1004.
+  llama3-70b-256req-bf16     Llama-3-70B KV (80 layers, 8 KV heads), bf16: 256
+                             requests of U{64..2048} tokens; 20480-page pools;
+                             a seeded permutation of the source pool dealt to
+                             requests round-robin one page at a time; moved in
+                             8-layer chunks.  Seed 1005.
+  llama3-8b-4096tok-bf16     Llama-3-8B KV, bf16: one 4096-token request (256
+                             pages) in a 2048-page pool (the promote-latency
+                             workload).  Seed 1100.
 """
 from __future__ import annotations
 
@@ -121,16 +126,25 @@ def _lifo_tables(free_list: List[int], lengths: List[int], page_size: int) -> Li
     return tables
 
 
-def config(c) -> Workload:
-    if c == 1:
+# The migration workloads, smallest first; the default benchmark workload is
+# the 16-request batch.
+NAMES = ("llama3-8b-512tok-fp16", "llama3-8b-16req-bf16", "llama2-7b-8x4095tok-fp16",
+         "llama3-8b-32768tok-bf16", "llama3-70b-256req-bf16")
+DEFAULT = "llama3-8b-16req-bf16"
+PROMOTE = "llama3-8b-4096tok-bf16"
+
+
+def get(name: str) -> Workload:
+    """The workload called `name` (one of NAMES or PROMOTE)."""
+    if name == "llama3-8b-512tok-fp16":
         seed = 1001
         rng = np.random.default_rng(seed)
         shape = KVShape(**LLAMA3_8B, dtype=torch.float16)
         lengths = [512]
         tables = [rng.permutation(2048)[:32].tolist()]
-        return Workload("config1", "1 x 512-token request, Llama-3-8B KV, fp16, 2048-page pool",
+        return Workload(name, "1 x 512-token request, Llama-3-8B KV, fp16, 2048-page pool",
                         shape, 2048, 2048, lengths, tables, seed)
-    if c == 2:
+    if name == "llama3-8b-16req-bf16":
         seed = 1002
         rng = np.random.default_rng(seed)
         shape = KVShape(**LLAMA3_8B, dtype=torch.bfloat16)
@@ -138,29 +152,29 @@ def config(c) -> Workload:
         lengths = np.clip(np.rint(raw), 128, 8192).astype(int).tolist()
         free = rng.permutation(16384).tolist()
         tables = _lifo_tables(free, lengths, 16)
-        return Workload("config2", "16 requests, lognormal(median 1024, sigma 1.0) tokens clipped "
+        return Workload(name, "16 requests, lognormal(median 1024, sigma 1.0) tokens clipped "
                         "[128, 8192], Llama-3-8B KV, bf16, 16384-page pools, fragmented source free list",
                         shape, 16384, 16384, lengths, tables, seed)
-    if c == 3:
+    if name == "llama2-7b-8x4095tok-fp16":
         seed = 1003
         rng = np.random.default_rng(seed)
         shape = KVShape(num_layers=32, num_kv_heads=32, head_dim=128, page_size=16, dtype=torch.float16)
         lengths = [4095] * 8
         free = rng.permutation(4096).tolist()
         tables = _lifo_tables(free, lengths, 16)
-        return Workload("config3", "8 x 4095-token requests (partial last page), Llama-2-7B KV, fp16, "
+        return Workload(name, "8 x 4095-token requests (partial last page), Llama-2-7B KV, fp16, "
                         "4096-page pools, pinned-host round trip per layer",
                         shape, 4096, 4096, lengths, tables, seed, staging="pinned", layers_per_chunk=1)
-    if c == 4:
+    if name == "llama3-8b-32768tok-bf16":
         seed = 1004
         rng = np.random.default_rng(seed)
         shape = KVShape(**LLAMA3_8B, dtype=torch.bfloat16)
         lengths = [32768]
         tables = [rng.permutation(2048).tolist()]
-        return Workload("config4", "1 x 32768-token request, Llama-3-8B KV, bf16, values U[-4,4], "
+        return Workload(name, "1 x 32768-token request, Llama-3-8B KV, bf16, values U[-4,4], "
                         "2048-page pool in permuted order, on-device and pinned-host",
                         shape, 2048, 2048, lengths, tables, seed, init="uniform4", staging="both")
-    if c == 5:
+    if name == "llama3-70b-256req-bf16":
         seed = 1005
         rng = np.random.default_rng(seed)
         shape = KVShape(num_layers=80, num_kv_heads=8, head_dim=128, page_size=16, dtype=torch.bfloat16)
@@ -174,18 +188,18 @@ def config(c) -> Workload:
                 if len(tables[r]) < need[r]:
                     tables[r].append(perm[k])
                     k += 1
-        return Workload("config5", "256 requests U{64..2048} tokens, Llama-3-70B KV (80 layers), bf16, "
+        return Workload(name, "256 requests U{64..2048} tokens, Llama-3-70B KV (80 layers), bf16, "
                         "20480-page pools dealt round-robin (heavily fragmented), 8-layer chunks",
                         shape, 20480, 20480, lengths, tables, seed, device_layers_per_chunk=8)
-    if c == "promote4k":
+    if name == PROMOTE:
         seed = 1100
         rng = np.random.default_rng(seed)
         shape = KVShape(**LLAMA3_8B, dtype=torch.bfloat16)
         lengths = [4096]
         tables = [rng.permutation(2048)[:256].tolist()]
-        return Workload("promote4k", "1 x 4096-token request, Llama-3-8B KV, bf16, 2048-page pools",
+        return Workload(name, "1 x 4096-token request, Llama-3-8B KV, bf16, 2048-page pools",
                         shape, 2048, 2048, lengths, tables, seed)
-    raise ValueError(f"unknown workload {c!r}")
+    raise ValueError(f"unknown workload {name!r} (known: {', '.join(NAMES + (PROMOTE,))})")
 
 
 def fill_pool(layers_pages: int, shape: KVShape, seed: int, init: str, device) -> List[torch.Tensor]:

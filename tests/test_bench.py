@@ -45,7 +45,7 @@ def test_summarize_pmc_scales_counters_by_the_calibration_copy(tmp_path):
     write = [{"Kernel_Name": COPY, "Counter_Name": "WRITE_SIZE", "Counter_Value": 2000.0},
              {"Kernel_Name": COPY_T, "Counter_Name": "WRITE_SIZE", "Counter_Value": 2000.0},
              {"Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": "WRITE_SIZE", "Counter_Value": gib_kib}]
-    d = bench.summarize_pmc(write_csv(tmp_path / "f.csv", fetch), write_csv(tmp_path / "w.csv", write), "config1")
+    d = bench.summarize_pmc(write_csv(tmp_path / "f.csv", fetch), write_csv(tmp_path / "w.csv", write), "llama3-8b-512tok-fp16")
     assert d["fetch_scale"] == 2.0 and d["write_scale"] == 1.0     # the 4 KiB copy is not a calibration
     assert d["fetch_bytes_per_launch"] == 2000 * 1024
     assert d["write_bytes_per_launch"] == 2000 * 1024
@@ -58,15 +58,15 @@ def test_summarize_pmc_needs_both_kinds_of_dispatch(tmp_path):
     rows = [{"Kernel_Name": COPY, "Counter_Name": "FETCH_SIZE", "Counter_Value": 1.0}]
     path = write_csv(tmp_path / "f.csv", rows)
     with pytest.raises(SystemExit):
-        bench.summarize_pmc(path, path, "config2")
+        bench.summarize_pmc(path, path, "llama3-8b-16req-bf16")
 
 
 def test_pmc_markdown_states_algorithmic_bytes_per_layer_chunk(tmp_path):
     from paceserve_amd import workloads
 
-    w = workloads.config(5)
+    w = workloads.get("llama3-70b-256req-bf16")
     alg = 2 * 8 * w.n_pages * w.shape.page_bytes          # one launch = one 8-layer chunk
-    t = {"workload": "config5", "kernel": "page_copy_kernel<false, false>",
+    t = {"workload": "llama3-70b-256req-bf16", "kernel": "page_copy_kernel<false, false>",
          "fetch_kib_per_dispatch_raw": 1.0, "fetch_calibration_kib_raw": 2.0, "fetch_scale": 2.0,
          "fetch_bytes_per_launch": alg // 2, "fetch_dispatches": 3, "write_kib_per_dispatch_raw": 1.0,
          "write_calibration_kib_raw": 1.0, "write_scale": 1.0, "write_bytes_per_launch": alg // 2,
@@ -76,7 +76,7 @@ def test_pmc_markdown_states_algorithmic_bytes_per_layer_chunk(tmp_path):
     md = bench.pmc_markdown(str(path))
     assert f"Algorithmic bytes per launch: {alg} (8 layers x {w.n_pages} pages" in md
     assert "= 1.00000 x algorithmic" in md
-    assert "--workload 5" in md
+    assert "--workload llama3-70b-256req-bf16" in md
 
 
 def test_timed_dispatches_skip_warmup_and_later_passes(tmp_path):

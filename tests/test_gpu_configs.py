@@ -7,9 +7,10 @@ the HIP path, then check
   - untouched destination pages and the whole source pool are unchanged: a
     checksum of per-layer word sums must move by exactly the touched pages'
     contribution (sum_after = sum_before - old touched pages + new pages);
-  - config 1 additionally against the CPU oracle, config 2 additionally
-    against an exact torch index_copy_ of a clone of the destination pool,
-    configs 3 and 4 also through the pinned-host round trip.
+  - the 512-token request additionally against the CPU oracle, the
+    16-request batch additionally against an exact torch index_copy_ of a
+    clone of the destination pool, the 8 x 4095-token and 32768-token
+    requests also through the pinned-host round trip.
 """
 import gc
 
@@ -46,7 +47,7 @@ def pages_sum(t, ids):
 
 
 def setup(c, dev):
-    w = workloads.config(c)
+    w = workloads.get(c)
     free_gb = torch.cuda.mem_get_info(dev)[0] / 1e9
     need_gb = (w.src_pool_pages + w.dst_pool_pages) * w.shape.num_layers * w.shape.page_bytes / 1e9
     if need_gb > 0.9 * free_gb:
@@ -83,16 +84,17 @@ def run_buffer(w, src, dst, plan, dev):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("c", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("c", workloads.NAMES)
 def test_workload_buffer_path(gpu, c):
     w, src, dst, plan, s_ids, d_ids = setup(c, gpu)
     print(f"{w.name}: {plan.n_pages} pages x {w.shape.num_layers} layers", flush=True)
     before = sums_before(src, dst, s_ids, d_ids)
     exact = None
-    if c == 2:      # exact expected destination for one layer set
+    if c == "llama3-8b-16req-bf16":      # exact expected destination for one layer set
         exact = [words(d).clone().index_copy_(0, d_ids, words(s).index_select(0, s_ids))
                  for s, d in zip(src.layers[:4], dst.layers[:4])]
-    if c == 1:      # CPU oracle on the full (small) workload
+    small = w.payload_bytes <= 64 << 20
+    if small:       # CPU oracle on the full (small) workload
         np_src = [words(s).cpu().numpy() for s in src.layers]
         np_dst = [words(d).cpu().numpy() for d in dst.layers]
         want = orc.move(np_src, plan.src_ids, np_dst, plan.dst_ids)
@@ -101,12 +103,12 @@ def test_workload_buffer_path(gpu, c):
     if exact is not None:
         for l in range(4):
             assert torch.equal(words(dst.layers[l]), exact[l]), f"layer {l} differs from index_copy_"
-    if c == 1:
+    if small:
         for l in range(w.shape.num_layers):
             np.testing.assert_array_equal(words(dst.layers[l]).cpu().numpy(), want[l])
 
 
-@pytest.mark.parametrize("c", [3, 4])
+@pytest.mark.parametrize("c", ["llama2-7b-8x4095tok-fp16", "llama3-8b-32768tok-bf16"])
 def test_workload_pinned_roundtrip(gpu, c):
     w, src, dst, plan, s_ids, d_ids = setup(c, gpu)
     before = sums_before(src, dst, s_ids, d_ids)
@@ -122,15 +124,15 @@ def test_workload_pinned_roundtrip(gpu, c):
 
 
 def test_workload_fused_move_matches(gpu):
-    w, src, dst, plan, s_ids, d_ids = setup(2, gpu)
+    w, src, dst, plan, s_ids, d_ids = setup("llama3-8b-16req-bf16", gpu)
     before = sums_before(src, dst, s_ids, d_ids)
     ops.move(src, plan.src_ids, dst, plan.dst_ids)
     torch.cuda.synchronize()
-    check_after(src, dst, s_ids, d_ids, before, "config2 fused")
+    check_after(src, dst, s_ids, d_ids, before, f"{w.name} fused")
 
 
 def test_promote_4k_all_modes(gpu):
-    w = workloads.config("promote4k")
+    w = workloads.get(workloads.PROMOTE)
     src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, gpu)
     outs = {}
     for mode in ("buffer", "fused", "pinned"):

@@ -135,7 +135,7 @@ def test_swap_space_orders_work_across_streams(gpu):
 
 
 def test_swap_4k_request(gpu):
-    w = workloads.config("promote4k")
+    w = workloads.get(workloads.PROMOTE)
     dev = ops.PagedPool(workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, gpu))
     host = ops.HostPagePool.like(dev, 256)
     ids = w.src_tables[0]
