@@ -264,6 +264,40 @@ def run_ceiling(w, dev, src, dst, n: int, reps: int = 10) -> dict:
     return {"identity_ids_gbs": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def run_torch_device(w, dev, src, dst, s_ids, d_ids, reps: int = 3) -> dict:
+    """The reference's own indexing, run on the device, layer by layer:
+    buf = src[l][ids] (KVhelper.get_kv_cache's gather,
+    paceserve/kv_transfer/kv_utils.py:44-46, without its host copy) and
+    dst[l][dst_ids] = buf (insert_kv_cache's index_put_, kv_utils.py:51-52,
+    without its host copy).  It writes the same bytes as the HIP path, so
+    the destination stays verified."""
+    import torch
+
+    L = w.shape.num_layers
+    si, di = s_ids.long(), d_ids.long()
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        for l in range(L):
+            buf = src.layers[l][si]
+            dst.layers[l][di] = buf
+
+    step()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        step()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    gbs = 4 * w.payload_bytes / (ms / 1e3) / 1e9
+    log(f"torch device indexing (per layer): {gbs:.1f} GB/s")
+    return {"value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 4), "steps": reps,
+            "launches_per_step": 2 * L,
+            "what": "per layer: buf = src[l][ids]; dst[l][dst_ids] = buf (torch advanced indexing on the device)"}
+
+
 def link_settle(dev, target_gbs: float = 45.0, max_wait_s: float = 30.0, streak: int = 3) -> dict:
     """Waits until `streak` consecutive 64 MiB pinned device-to-host copies,
     0.2 s apart, each run at target_gbs or more (other DMA work, such as the
@@ -720,6 +754,7 @@ def main():
         res["verified"] = verify(w, src, dst, s_ids, d_ids, dev)
         log(f"verified: {res['verified']}")
     ceiling = run_ceiling(w, dev, src, dst, plan.n_pages) if args.mode == "buffer" else None
+    torch_dev = run_torch_device(w, dev, src, dst, s_ids, d_ids)
     if args.calibrate:
         run_calibration(dev)
     cpu = None
@@ -768,6 +803,7 @@ def main():
         "unpack_ms": res["unpack_ms_mean"],
         "roofline": res["roofline"],
         "copy_ceiling": ceiling,
+        "torch_device_baseline": torch_dev,
         "promote_4k": promote,
         "staging": staging,
         "cpu_baseline": cpu,
