@@ -67,6 +67,9 @@ def parse_args():
                     help="also time the pinned-host round trip (default for workloads 3 and 4)")
     ap.add_argument("--no-staging", action="store_true",
                     help="skip the pinned-host round trip, also for workloads 3 and 4")
+    ap.add_argument("--dropin", action="store_true",
+                    help="also time KVhelper get_kv_cache + insert_kv_cache against the reference's torch code "
+                         "for the same calls (4096-token request)")
     return ap.parse_args()
 
 
@@ -296,6 +299,106 @@ def run_torch_device(w, dev, src, dst, s_ids, d_ids, reps: int = 3) -> dict:
     return {"value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 4), "steps": reps,
             "launches_per_step": 2 * L,
             "what": "per layer: buf = src[l][ids]; dst[l][dst_ids] = buf (torch advanced indexing on the device)"}
+
+
+class _DropinModel:
+    """Duck-typed model/cache configs and model runner for KVhelper: it reads
+    only these attributes (paceserve/kv_transfer/kv_utils.py:17-23)."""
+
+    def __init__(self, shape, cache):
+        self.shape, self.dtype, self.block_size = shape, shape.dtype, shape.page_size
+
+        class _Wrapper:
+            gpu_cache = cache
+
+        self.attention_backend_wrapper = _Wrapper()
+
+    def get_num_q_heads(self, pc):
+        return 4 * self.shape.num_kv_heads
+
+    def get_num_kv_heads(self, pc):
+        return self.shape.num_kv_heads
+
+    def get_head_size(self):
+        return self.shape.head_dim
+
+    def get_num_layers(self, pc):
+        return self.shape.num_layers
+
+
+def run_dropin(dev, steps: int = 10, warmup: int = 2) -> dict:
+    """The drop-in KVhelper moving the 4096-token request from one cache to
+    another through host memory (get_kv_cache, then insert_kv_cache), against
+    the reference's code for the same two calls written with torch: a
+    pageable torch.zeros host tensor filled layer by layer from
+    gpu_cache[i][tensor(ids)] (paceserve/kv_transfer/kv_utils.py:44-46), then
+    gpu_cache[i][tensor(ids)] = content[i].to(device) per layer (:51-52).
+    Wall-clock per call pair, to completion; both must leave the same bytes."""
+    import torch
+
+    from paceserve_amd import workloads
+    from paceserve_amd.kv_transfer.kv_utils import KVhelper
+
+    w = workloads.get(workloads.PROMOTE)
+    L, n = w.shape.num_layers, w.n_pages
+    src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev)
+    dst = workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev)
+    ids = list(w.src_tables[0])
+    dst_ids = list(range(w.dst_pool_pages - 1, w.dst_pool_pages - 1 - n, -1))   # a fresh LIFO pool's pages
+
+    def helper(cache):
+        import contextlib
+
+        m = _DropinModel(w.shape, cache)
+        with contextlib.redirect_stdout(sys.stderr):       # KVhelper announces itself, as the reference does
+            h = KVhelper(0, m, m, None)
+        h.add_model_runner(m)
+        return h
+
+    class _Seq:
+        seq_id = "r"
+
+    class _Tables:
+        def _get_block_table(self, seq):
+            return ids
+
+    src_h, dst_h = helper(src), helper(dst)
+
+    def ours():
+        content, _ = src_h.get_kv_cache(_Seq(), _Tables())
+        if not dst_h.insert_kv_cache(content, dst_ids, dev):
+            raise RuntimeError("insert_kv_cache failed")
+
+    def reference():
+        seq_cache = torch.zeros((L, n) + w.shape.page_shape, dtype=w.shape.dtype)
+        for i in range(L):
+            seq_cache[i] = src[i][torch.tensor(ids), :, :, :, :]
+        for i in range(L):
+            dst[i][torch.tensor(dst_ids), :, :, :, :] = seq_cache[i].to(dev)
+
+    out = {"payload_bytes": w.payload_bytes, "workload": w.name, "runs": steps}
+    for name, fn in (("kvhelper", ours), ("reference_torch", reference)):
+        ts = []
+        for i in range(warmup + steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            if i >= warmup:
+                ts.append(time.perf_counter() - t0)
+        ms = statistics.median(ts) * 1e3
+        out[f"{name}_ms"] = round(ms, 2)
+        out[f"{name}_gbs_per_direction"] = round(w.payload_bytes / (ms / 1e3) / 1e9, 2)
+        log(f"drop-in {name}: {ms:.2f} ms per get + insert")
+        if name == "kvhelper":
+            after = [d[torch.tensor(dst_ids, device=dev)].view(torch.int16).clone() for d in dst]
+            for d in dst:
+                d.zero_()
+    ok = all(torch.equal(d[torch.tensor(dst_ids, device=dev)].view(torch.int16), a) for d, a in zip(dst, after))
+    ok = ok and all(torch.equal(s[torch.tensor(ids, device=dev)].view(torch.int16), a) for s, a in zip(src, after))
+    out["same_bytes"] = ok
+    out["speedup"] = round(out["reference_torch_ms"] / out["kvhelper_ms"], 2)
+    return out
 
 
 def link_settle(dev, target_gbs: float = 45.0, max_wait_s: float = 30.0, streak: int = 3) -> dict:
@@ -779,6 +882,9 @@ def main():
         if not args.no_promote:
             promote = run_promote(dev)
             promote["link_probe"] = settle
+    dropin = None
+    if args.dropin:
+        dropin = run_dropin(dev)
     del src, dst, s_ids, d_ids
     torch.cuda.empty_cache()
 
@@ -806,6 +912,7 @@ def main():
         "torch_device_baseline": torch_dev,
         "promote_4k": promote,
         "staging": staging,
+        "dropin": dropin,
         "cpu_baseline": cpu,
     }
     tr = traffic_from_profiles(w.name) if args.mode == "buffer" else None
