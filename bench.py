@@ -67,9 +67,9 @@ def parse_args():
                     help="also time the pinned-host round trip (default for workloads 3 and 4)")
     ap.add_argument("--no-staging", action="store_true",
                     help="skip the pinned-host round trip, also for workloads 3 and 4")
-    ap.add_argument("--dropin", action="store_true",
-                    help="also time KVhelper get_kv_cache + insert_kv_cache against the reference's torch code "
-                         "for the same calls (4096-token request)")
+    ap.add_argument("--no-dropin", action="store_true",
+                    help="skip timing KVhelper get_kv_cache + insert_kv_cache against the reference's torch "
+                         "code for the same calls (4096-token request)")
     return ap.parse_args()
 
 
@@ -883,8 +883,10 @@ def main():
             promote = run_promote(dev)
             promote["link_probe"] = settle
     dropin = None
-    if args.dropin:
+    if not args.no_dropin:
+        settle = link_settle(dev)       # the promote leg has just freed its pools
         dropin = run_dropin(dev)
+        dropin["link_probe"] = settle
     del src, dst, s_ids, d_ids
     torch.cuda.empty_cache()
 
