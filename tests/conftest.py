@@ -13,6 +13,18 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built libpace_kv.so")
 
 
+def pytest_sessionstart(session):
+    """Builds libpace_kv.so and the C checker when a checkout has neither
+    (they are build outputs, not sources); a tree that has them is used as
+    it is."""
+    from paceserve_amd import build
+
+    if not build.LIB_PATH.exists():
+        build.build_library()
+    if not build.C_CHECK_BIN.exists():
+        build.build_c_check()
+
+
 def gpu_available() -> bool:
     if not os.path.exists("/dev/kfd"):
         return False
