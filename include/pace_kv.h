@@ -146,8 +146,9 @@ int pace_kv_swap_in(const void* const* host_layers, int64_t host_pool_pages,
 
 /*
  * A stager owns two rings of device slots (one feeding device-to-host copies,
- * one fed by host-to-device copies), two side streams (D2H and H2D, default
- * priority) and the events that order them against the caller's stream.
+ * one fed by host-to-device copies), three side streams (D2H copies, H2D
+ * copies and the round trip's unpacks; default priority) and the events that
+ * order them against the caller's stream.
  * Each slot holds slot_bytes; a layer chunk of k layers needs
  * k * n_pages * page_bytes <= slot_bytes.
  */

@@ -301,8 +301,9 @@ class Promoter:
 
 
 class Stager:
-    """Pinned-host staging pipeline (pace_kv_stager): device slot rings, a D2H
-    and an H2D side stream, and the events that order them.
+    """Pinned-host staging pipeline (pace_kv_stager): device slot rings, side
+    streams for D2H copies, H2D copies and the round trip's unpacks, and the
+    events that order them.
 
     Host tensors handed to a call are kept alive until the caller's stream has
     passed the point where the call's copies finish.  One host thread at a
