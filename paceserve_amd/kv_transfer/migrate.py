@@ -192,15 +192,25 @@ class KVMigrator:
             raise TypeError("promote_native needs a NativeBlockAllocator")
         if self._promoter is None:
             self._promoter = ops.Promoter(self.src.device)
-        buf = None
+        if mode not in ("buffer", "fused"):
+            raise ValueError(f"promote_native supports modes 'buffer' and 'fused', not {mode!r}")
+        src_ids = np.ascontiguousarray(src_ids, dtype=np.int32)
+        indptr = np.ascontiguousarray(indptr, dtype=np.int64)
+        n = int(indptr[-1])
+        if dst_pages is None:
+            counts, total = None, n
+        else:
+            counts = np.ascontiguousarray(dst_pages, dtype=np.int32)
+            total = int(counts.sum())
+        buf_ptr, stride, blayers = None, 0, 0
         if mode == "buffer":
-            n = int(indptr[-1])
+            # The migrator's own view: contiguous [k, n, *page_shape] of the
+            # pools' dtype on their device, so it needs no further checks.
             k = layers_per_chunk or self.chunk_layers(n)
             buf = self._buffer(min(k, self.src.num_layers), n)
-        elif mode != "fused":
-            raise ValueError(f"promote_native supports modes 'buffer' and 'fused', not {mode!r}")
-        return self._promoter.promote(self.src, self.dst, self.dst_allocator, src_ids, indptr,
-                                      dst_pages, buf)
+            buf_ptr, stride, blayers = buf.data_ptr(), n * self.src.page_bytes, int(buf.shape[0])
+        return self._promoter._launch(self.src, self.dst, self.dst_allocator, src_ids, indptr, counts, total,
+                                      buf_ptr, stride, blayers)
 
     def promote(self, src_tables: Sequence[Sequence[int]], dst_pages: Optional[Sequence[int]] = None,
                 mode: str = "buffer", layers_per_chunk: Optional[int] = None,

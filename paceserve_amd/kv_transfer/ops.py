@@ -19,6 +19,7 @@ from __future__ import annotations
 import ctypes
 from typing import List, Optional, Sequence, Tuple, Union
 
+import numpy as np
 import torch
 
 from .. import _native
@@ -255,8 +256,6 @@ class Promoter:
                 buffer: Optional[torch.Tensor] = None, err: Optional[torch.Tensor] = None):
         """Returns every request's destination table, concatenated (int32
         numpy array; request r owns dst_pages[r] entries)."""
-        import numpy as np
-
         sp, dp = as_pool(src), as_pool(dst)
         if sp is not dp and (not sp.compatible(dp) or sp.num_layers != dp.num_layers):
             raise ValueError("source and destination pools differ in layout, layers, dtype or device")
@@ -270,16 +269,23 @@ class Promoter:
         else:
             counts = np.ascontiguousarray(dst_pages, dtype=np.int32)
             total = int(counts.sum())
-        tables = np.empty(max(total, 1), dtype=np.int32)
         buf_ptr, stride, blayers = None, 0, 0
         if buffer is not None:
             stride = _check_buffer(buffer, sp, 1, src_ids.size, "promote")
             buf_ptr, blayers = buffer.data_ptr(), int(buffer.shape[0])
+        return self._launch(sp, dp, allocator, src_ids, indptr, counts, total, buf_ptr, stride, blayers, err)
+
+    def _launch(self, sp: PagedPool, dp: PagedPool, allocator, src_ids, indptr, counts, total: int,
+                buf_ptr: Optional[int], stride: int, blayers: int, err: Optional[torch.Tensor] = None):
+        """The library call with arguments already checked: src_ids int32 and
+        indptr int64 contiguous numpy arrays, counts (int32) or None, the
+        buffer as pointer / layer stride / layers (or None, 0, 0)."""
+        tables = np.empty(max(total, 1), dtype=np.int32)
         rc = _native.load().pace_kv_promote(
             self._handle, allocator.handle, sp.table(), sp.num_pages, dp.table(), dp.num_pages,
             sp.num_layers, sp.page_bytes, indptr.size - 1, indptr.ctypes.data,
             src_ids.ctypes.data if src_ids.size else None,
-            None if dst_pages is None else counts.ctypes.data, buf_ptr, stride, blayers,
+            None if counts is None else counts.ctypes.data, buf_ptr, stride, blayers,
             tables.ctypes.data, _err_ptr(err), _stream_handle(sp.device))
         if rc == _native.PACE_KV_ENOMEM:
             from ..core.block_manager import OOM_MESSAGE
