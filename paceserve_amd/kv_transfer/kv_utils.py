@@ -24,6 +24,7 @@ leg (pack_pages / unpack_pages).
 """
 from __future__ import annotations
 
+import threading
 from typing import List, Optional, Sequence
 
 import torch
@@ -99,6 +100,13 @@ class KVhelper:
         self.model_runner = None
         self._pool: Optional[ops.PagedPool] = None
         self._stager: Optional[ops.Stager] = None
+        # The reference calls get_kv_cache / insert_kv_cache from several
+        # threads of one worker at once (Ray max_concurrency=8,
+        # paceserve/engine/base_llm_engine.py:32,166-177; 4+4 insertion
+        # threads, paceserve/disutil/decode_instance.py:50-51).  The staging
+        # pipeline and the pool table are shared, so a call holds this lock
+        # until its copies have finished.
+        self._lock = threading.RLock()
         print(f"kv helper initialized on worker: {self.rank}")
 
     # ---------------------------------------------------------------- pools
@@ -111,10 +119,11 @@ class KVhelper:
 
     def pool(self) -> ops.PagedPool:
         """The bound cache as a PagedPool (rebuilt when its tensors change)."""
-        cache = self._gpu_cache()
-        if self._pool is None or not self._pool.holds(cache):
-            self._pool = ops.PagedPool(cache[: self.num_layers])
-        return self._pool
+        with self._lock:
+            cache = self._gpu_cache()
+            if self._pool is None or not self._pool.holds(cache):
+                self._pool = ops.PagedPool(cache[: self.num_layers])
+            return self._pool
 
     def _stager_for(self, pool: ops.PagedPool, slot_bytes: int) -> ops.Stager:
         st = self._stager
@@ -131,10 +140,11 @@ class KVhelper:
         return (2, self.block_size, self.num_kv_heads, self.head_dim)
 
     def reset_kv_cache(self, num_gpu_blocks: int) -> None:
-        cache = self._gpu_cache()
-        for i in range(self.num_layers):
-            cache[i] = torch.zeros(num_gpu_blocks, *self.page_shape(), dtype=self.dtype, device="cuda")
-        self._pool = None
+        with self._lock:
+            cache = self._gpu_cache()
+            for i in range(self.num_layers):
+                cache[i] = torch.zeros(num_gpu_blocks, *self.page_shape(), dtype=self.dtype, device="cuda")
+            self._pool = None
 
     # ------------------------------------------------------- reference API
 
@@ -148,21 +158,23 @@ class KVhelper:
         if not kv_page_indices:
             return torch.zeros(self.num_layers, 1, *self.page_shape(), dtype=self.dtype), [0]
 
-        pool = self.pool()
-        ids = normalize_page_ids(kv_page_indices, pool.num_pages)
-        n = len(ids)
-        host = torch.empty((self.num_layers, n) + pool.page_shape, dtype=pool.dtype, pin_memory=True)
-        layer_bytes = n * pool.page_bytes
-        k = chunk_layers(self.num_layers, layer_bytes)
-        with torch.cuda.device(pool.device):
-            stager = self._stager_for(pool, k * layer_bytes)
-            stager.pack_to_host(pool, ids, host, k)
-            torch.cuda.current_stream(pool.device).synchronize()
+        with self._lock:
+            pool = self.pool()
+            ids = normalize_page_ids(kv_page_indices, pool.num_pages)
+            n = len(ids)
+            host = torch.empty((self.num_layers, n) + pool.page_shape, dtype=pool.dtype, pin_memory=True)
+            layer_bytes = n * pool.page_bytes
+            k = chunk_layers(self.num_layers, layer_bytes)
+            with torch.cuda.device(pool.device):
+                stager = self._stager_for(pool, k * layer_bytes)
+                stager.pack_to_host(pool, ids, host, k)
+                torch.cuda.current_stream(pool.device).synchronize()
         return host, kv_page_indices
 
     def insert_kv_cache(self, cached_content, kv_indices, device) -> bool:
         try:
-            self._insert(cached_content, kv_indices, device)
+            with self._lock:
+                self._insert(cached_content, kv_indices, device)
             return True
         except Exception as e:  # the reference's convention: report, never raise
             print(f"error during insert kv cache: {e}")

@@ -24,6 +24,7 @@ is byte-identical to what the reference's get_kv_cache returns for it.
 from __future__ import annotations
 
 import itertools
+import threading
 from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
@@ -115,6 +116,12 @@ class KVMigrator:
         self._buf_view: Optional[torch.Tensor] = None
         self._elem = self.src.layers[0].element_size()
         self._promoter: Optional[ops.Promoter] = None
+        # One migrator may be driven from several threads and streams: the
+        # lock covers its host state (buffer, stager, promoter), and a call
+        # on a stream other than the last user's first waits for that
+        # stream's work, since the transfer buffer is shared.
+        self._lock = threading.RLock()
+        self._buf_stream: Optional[torch.cuda.Stream] = None
 
     # ------------------------------------------------------------ planning
 
@@ -134,9 +141,21 @@ class KVMigrator:
 
     # ------------------------------------------------------------ movement
 
+    def _order_after_last_user(self) -> None:
+        """Orders the current stream after the stream that last used the
+        transfer buffer (and lets torch's allocator know the buffer is used
+        here), when the two differ.  Caller holds the lock."""
+        stream = torch.cuda.current_stream(self.src.device)
+        if self._buf_stream is not None and self._buf_stream != stream:
+            stream.wait_stream(self._buf_stream)
+            if self._buf is not None:
+                self._buf.record_stream(stream)
+        self._buf_stream = stream
+
     def _buffer(self, layers: int, n: int) -> torch.Tensor:
         """A [layers, n, *page_shape] view of the migrator's transfer buffer
-        (grown on demand; the last view is reused for the same shape)."""
+        (grown on demand; the last view is reused for the same shape).
+        Caller holds the lock and has called _order_after_last_user."""
         v = self._buf_view
         if v is not None and v.shape[0] == layers and v.shape[1] == n:
             return v
@@ -155,9 +174,14 @@ class KVMigrator:
     def move_pages(self, src_ids: torch.Tensor, dst_ids: torch.Tensor, mode: str = "buffer",
                    layers_per_chunk: Optional[int] = None,
                    host_buf: Optional[torch.Tensor] = None) -> None:
+        with self._lock:
+            self._move_pages(src_ids, dst_ids, mode, layers_per_chunk, host_buf)
+
+    def _move_pages(self, src_ids, dst_ids, mode, layers_per_chunk, host_buf) -> None:
         n = src_ids.numel()
         if n == 0:
             return
+        self._order_after_last_user()
         L = self.src.num_layers
         if mode == "fused":
             ops.move(self.src, src_ids, self.dst, dst_ids)
@@ -190,10 +214,15 @@ class KVMigrator:
         Returns the destination tables concatenated (int32 array)."""
         if not isinstance(self.dst_allocator, NativeBlockAllocator):
             raise TypeError("promote_native needs a NativeBlockAllocator")
+        with self._lock:
+            return self._promote_native(src_ids, indptr, dst_pages, mode, layers_per_chunk)
+
+    def _promote_native(self, src_ids, indptr, dst_pages, mode, layers_per_chunk):
         if self._promoter is None:
             self._promoter = ops.Promoter(self.src.device)
         if mode not in ("buffer", "fused"):
             raise ValueError(f"promote_native supports modes 'buffer' and 'fused', not {mode!r}")
+        self._order_after_last_user()
         src_ids = np.ascontiguousarray(src_ids, dtype=np.int32)
         indptr = np.ascontiguousarray(indptr, dtype=np.int64)
         n = int(indptr[-1])

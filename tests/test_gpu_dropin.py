@@ -195,3 +195,45 @@ def test_worker_migration_end_to_end(gpu, tokens_src, tokens_dst):
                            words(src_cache[l][torch.tensor(src_table, device=gpu)]))
         untouched = sorted(set(range(POOL)) - set(dst_table[:n]))
         assert torch.equal(words(dst_cache[l][untouched]), dst_before[l][untouched])
+
+
+def test_concurrent_inserts_and_gets_from_worker_threads(gpu):
+    # The reference inserts from up to 8 threads of one worker at once
+    # (decode_instance.py:50-51, Ray max_concurrency=8).  Requests of
+    # different sizes make later calls grow the shared staging pipeline
+    # while other threads wait for it.
+    import threading
+
+    h, cache = make_helper(gpu, torch.bfloat16, seed=7)
+    src_h, src_cache = make_helper(gpu, torch.bfloat16, seed=8)
+    perm = np.random.default_rng(9).permutation(POOL).tolist()
+    sizes = [1, 3, 8, 2, 12, 5, 9, 4]                      # 44 pages, disjoint
+    tables, pos = [], 0
+    for k in sizes:
+        tables.append(perm[pos:pos + k])
+        pos += k
+    contents = [torch.randn(L, k, 2, P, H, D).to(torch.bfloat16) for k in sizes]
+    contents = [c.pin_memory() if i % 2 == 0 else c for i, c in enumerate(contents)]   # pinned and pageable
+    got, errors = {}, []
+
+    def insert(i):
+        try:
+            if not h.insert_kv_cache(contents[i], tables[i], gpu):
+                errors.append((i, "insert returned False"))
+            out, ids = src_h.get_kv_cache(Sequence.of_length(f"s{i}", 16 * sizes[i], P), _SeqManager(tables[i]))
+            got[i] = out
+        except Exception as e:                             # reported by the main thread
+            errors.append((i, repr(e)))
+
+    ts = [threading.Thread(target=insert, args=(i,)) for i in range(len(sizes))]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for i, table in enumerate(tables):
+        idx = torch.tensor(table, device=gpu)
+        for l in range(L):
+            assert torch.equal(words(cache[l][idx]).cpu(), words(contents[i][l])), f"insert {i} layer {l}"
+            assert torch.equal(words(got[i][l]), words(src_cache[l][idx]).cpu()), f"get {i} layer {l}"

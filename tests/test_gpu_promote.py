@@ -89,3 +89,45 @@ def test_native_promote_out_of_pages_leaves_allocator_unchanged(gpu):
     torch.cuda.synchronize()
     for l in range(SHAPE.num_layers):
         assert torch.equal(words(dst8.layers[l]), before[l])
+
+
+def test_one_migrator_from_threads_on_their_own_streams(gpu):
+    # Two threads promote through one migrator (its transfer buffer is
+    # shared) on streams of their own, with no host synchronisation between.
+    import threading
+
+    src, dst = pools(gpu, 21)
+    rng = np.random.default_rng(22)
+    perm = rng.permutation(POOL).tolist()
+    batches = [[perm[i * 40:(i + 1) * 40]] for i in range(8)]          # disjoint 40-page requests
+    for native in (False, True):
+        alloc = (NativeBlockAllocator if native else BlockAllocator)(16, POOL)
+        mig = migrate.KVMigrator(src, dst, alloc)
+        plans, errors = {}, []
+
+        def worker(t):
+            try:
+                stream = torch.cuda.Stream(gpu)
+                with torch.cuda.stream(stream):
+                    for i in range(t, len(batches), 2):
+                        plans[i] = mig.promote(batches[i], mode="buffer")
+                stream.synchronize()
+            except Exception as e:                                     # reported by the main thread
+                errors.append((t, repr(e)))
+
+        ts = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+        for t in ts:
+            t.start()
+        for t in ts:
+            t.join()
+        torch.cuda.synchronize()
+        assert not errors, errors
+        for i, plan in plans.items():
+            s_ids = torch.tensor(plan.src_ids, device=gpu)
+            d_ids = torch.tensor(plan.dst_ids, device=gpu)
+            for l in range(SHAPE.num_layers):
+                assert torch.equal(words(src.layers[l]).index_select(0, s_ids),
+                                   words(dst.layers[l]).index_select(0, d_ids)), f"native={native} batch {i}"
+        for plan in plans.values():
+            for t in plan.dst_tables:
+                alloc.free_many(reversed(t))
