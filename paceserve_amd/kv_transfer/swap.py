@@ -11,6 +11,7 @@ back into newly allocated device pages, after which the host pages are free.
 """
 from __future__ import annotations
 
+import threading
 from typing import Dict, List, Optional
 
 import torch
@@ -32,6 +33,10 @@ class SwapSpace:
         # Recorded after each swap-in: host pages it freed are reused only by
         # work ordered after it, whichever stream that work runs on.
         self._swapped_in: Optional[torch.cuda.Event] = None
+        # The reference swaps in from several insertion threads while its
+        # engine thread swaps out (paceserve/disutil/decode_instance.py:50-51,
+        # paceserve/engine/decode_llm_engine.py:31-41).
+        self._lock = threading.Lock()
 
     def num_free_host_pages(self) -> int:
         return self.host_allocator.get_num_free_blocks()
@@ -39,6 +44,10 @@ class SwapSpace:
     def swap_out(self, seq_id: str, dev_table: List[int]) -> List[int]:
         """Copies the request's device pages into newly allocated host pages;
         the device pages stay allocated (the caller frees them)."""
+        with self._lock:
+            return self._swap_out(seq_id, dev_table)
+
+    def _swap_out(self, seq_id: str, dev_table: List[int]) -> List[int]:
         if seq_id in self.tables:
             raise ValueError(f"sequence {seq_id} is already swapped out")
         ids = normalize_page_ids(dev_table, self.dev.num_pages)
@@ -61,6 +70,10 @@ class SwapSpace:
         caller) and returns the host pages to the host allocator.  The copy
         waits for the request's swap_out, and a later swap_out, on any
         stream, waits for this copy before it writes host pages."""
+        with self._lock:
+            self._swap_in(seq_id, dev_table)
+
+    def _swap_in(self, seq_id: str, dev_table: List[int]) -> None:
         host_table = self.tables.pop(seq_id)
         ids = normalize_page_ids(dev_table, self.dev.num_pages)
         if len(ids) != len(host_table):
@@ -75,4 +88,5 @@ class SwapSpace:
         self.host_allocator.free_many(host_table)
 
     def holds(self, seq_id: str) -> bool:
-        return seq_id in self.tables
+        with self._lock:
+            return seq_id in self.tables
