@@ -67,6 +67,8 @@ def parse_args():
                     help="also time the pinned-host round trip (default for workloads 3 and 4)")
     ap.add_argument("--no-staging", action="store_true",
                     help="skip the pinned-host round trip, also for workloads 3 and 4")
+    ap.add_argument("--no-append", action="store_true",
+                    help="skip timing the paged-append producer kernel")
     ap.add_argument("--no-dropin", action="store_true",
                     help="skip timing KVhelper get_kv_cache + insert_kv_cache against the reference's torch "
                          "code for the same calls (4096-token request)")
@@ -223,15 +225,20 @@ TEMPORAL_STORE_MAX_BYTES = 1 << 30
 
 def copy_kernel_names(mode: str, launch_payload: int, page_bytes: int) -> str:
     """The page_copy_kernel instances a step launches (template arguments
-    GUARD = page not a multiple of 1 KiB rows, TEMPORAL = plain stores)."""
+    GUARD = page not a multiple of 1 KiB rows, TEMPORAL = plain stores,
+    POW2 = a power-of-two number of rows per page)."""
     guard = "true" if page_bytes % 1024 else "false"
+    rows = -(-page_bytes // 1024)
+    pow2 = "true" if rows & (rows - 1) == 0 else "false"
+
+    def k(temporal: str) -> str:
+        return f"page_copy_kernel<{guard}, {temporal}, {pow2}>"
+
     if mode == "fused":
-        return f"page_copy_kernel<{guard}, false> (move, nontemporal stores)"
-    temporal = launch_payload <= TEMPORAL_STORE_MAX_BYTES
-    if temporal:
-        return (f"page_copy_kernel<{guard}, true> (pack, plain stores) and "
-                f"page_copy_kernel<{guard}, false> (unpack, nontemporal stores)")
-    return f"page_copy_kernel<{guard}, false> (pack and unpack, nontemporal stores)"
+        return f"{k('false')} (move, nontemporal stores)"
+    if launch_payload <= TEMPORAL_STORE_MAX_BYTES:
+        return f"{k('true')} (pack, plain stores) and {k('false')} (unpack, nontemporal stores)"
+    return f"{k('false')} (pack and unpack, nontemporal stores)"
 
 
 def run_ceiling(w, dev, src, dst, n: int, reps: int = 10) -> dict:
@@ -299,6 +306,92 @@ def run_torch_device(w, dev, src, dst, s_ids, d_ids, reps: int = 3) -> dict:
     return {"value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 4), "steps": reps,
             "launches_per_step": 2 * L,
             "what": "per layer: buf = src[l][ids]; dst[l][dst_ids] = buf (torch advanced indexing on the device)"}
+
+
+def run_append(dev, steps: int = 50, warmup: int = 5) -> dict:
+    """The producer kernel (append_paged_kv_cache, NHD layout) on one
+    Llama-3-8B layer cache [2048 pages, 2, 16, 8, 128] bf16:
+      prefill: 16 requests x 1024 new tokens (16384 K and V rows);
+      decode:  256 requests x 1 new token, sequences of 1..64 tokens.
+    Algorithmic bytes per launch: each appended K and V row (8 * 128 * 2 B)
+    read once and written once.  Kernel time comes from replays of a HIP
+    graph of launches; the eager time per Python call is reported beside it.
+    Every appended row is checked against torch's own indexing of the cache
+    after the replays."""
+    import torch
+
+    from paceserve_amd.kv_transfer import append as ap
+
+    P, H, D, pages = 16, 8, 128, 2048
+    row = H * D * 2
+    g = torch.Generator(device=dev).manual_seed(1200)
+    cache = torch.randn((pages, 2, P, H, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    perm = torch.randperm(pages, generator=torch.Generator().manual_seed(1201)).to(torch.int32)
+    stream = torch.cuda.current_stream(dev)
+    out = {"cache": f"[{pages}, 2, {P}, {H}, {D}] bf16", "unit": "GB/s"}
+    lens_rng = torch.Generator().manual_seed(1202)
+    cases = {
+        "prefill": ([1024] * 16, [1024] * 16),
+        "decode": (torch.randint(1, 65, (256,), generator=lens_rng).tolist(), [1] * 256),
+    }
+    for name, (seq_lens, new) in cases.items():
+        npages = [-(-n // P) for n in seq_lens]
+        kv_indptr = torch.tensor([0] + list(torch.tensor(npages).cumsum(0).tolist()), dtype=torch.int32, device=dev)
+        kv_indices = perm[: int(kv_indptr[-1])].to(dev)
+        last = torch.tensor([n - (k - 1) * P for n, k in zip(seq_lens, npages)], dtype=torch.int32, device=dev)
+        append_indptr = torch.tensor([0] + list(torch.tensor(new).cumsum(0).tolist()), dtype=torch.int32, device=dev)
+        nnz = int(append_indptr[-1])
+        key = torch.randn((nnz, H, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        value = torch.randn((nnz, H, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        sl = ap.get_seq_lens(kv_indptr, last, P)
+        bi, pos = ap.get_batch_indices_positions(append_indptr, sl, nnz)
+
+        def launch():
+            ap.append_paged_kv_cache(key, value, bi, pos, cache, kv_indices, kv_indptr, last)
+
+        for _ in range(warmup):
+            launch()
+        torch.cuda.synchronize()
+
+        def timed(fn, reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(reps):
+                fn()
+            b.record(stream)
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / reps * 1e3
+
+        eager_us = timed(launch, steps)
+        # The Python wrapper costs more host time per call than a decode
+        # launch takes on the GPU, so the kernel is timed from a HIP graph of
+        # `steps` launches, replayed; it allocates nothing and records no
+        # memset, and every replay rewrites the same rows.
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            launch()
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            for _ in range(steps):
+                launch()
+        graph.replay()
+        torch.cuda.synchronize()
+        us = timed(graph.replay, 5) / steps
+        alg = 4 * nnz * row
+        # every appended row sits where the cache's page table puts it
+        b_l, p_l = bi.long(), pos.long()
+        page_t = kv_indices.long()[kv_indptr.long()[b_l] + p_l // P]
+        ok = torch.equal(cache[page_t, 0, p_l % P].view(torch.int16), key.view(torch.int16)) and \
+            torch.equal(cache[page_t, 1, p_l % P].view(torch.int16), value.view(torch.int16))
+        out[name] = {"tokens": nnz, "requests": len(seq_lens), "us_per_launch": round(us, 2),
+                     "eager_us_per_call": round(eager_us, 2),
+                     "algorithmic_bytes_per_launch": alg, "gbs": round(alg / (us * 1e-6) / 1e9, 1),
+                     "frac_of_hbm_peak": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "verified": bool(ok)}
+        log(f"append {name}: {nnz} tokens, {us:.2f} us per launch, {out[name]['gbs']} GB/s, verified {ok}")
+    return out
 
 
 class _DropinModel:
@@ -628,7 +721,7 @@ def _rows(csv_path: str) -> list:
 def _json(path: str) -> dict:
     with open(path) as f:
         return json.load(f)
-KERNEL_TAG = "page_copy_kernel<false, false>"
+KERNEL_TAG = "page_copy_kernel<false, false, true>"
 
 
 def _per_dispatch(csv_path: str, counter: str):
@@ -858,6 +951,7 @@ def main():
         log(f"verified: {res['verified']}")
     ceiling = run_ceiling(w, dev, src, dst, plan.n_pages) if args.mode == "buffer" else None
     torch_dev = run_torch_device(w, dev, src, dst, s_ids, d_ids)
+    append = None if args.no_append else run_append(dev)
     if args.calibrate:
         run_calibration(dev)
     cpu = None
@@ -912,6 +1006,7 @@ def main():
         "roofline": res["roofline"],
         "copy_ceiling": ceiling,
         "torch_device_baseline": torch_dev,
+        "append": append,
         "promote_4k": promote,
         "staging": staging,
         "dropin": dropin,

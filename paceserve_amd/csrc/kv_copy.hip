@@ -13,12 +13,13 @@
 // (K half then V half).  It is split into 1 KiB rows; one workgroup of one
 // wave64 copies one row, each lane moving one 16-byte vector with a
 // nontemporal load and a nontemporal store, and then retires.  The grid is
-// rows x pages x layers (blockIdx.x = row, .y = page, .z = layer), so a wave
-// finds its row without integer division, and workgroups, dispatched row
-// fastest, then page, then layer, read (unpack) or write (pack) adjacent rows
-// of the transfer buffer and adjacent rows of each pool page.  An unpack wave
-// issues its buffer load before its destination page id arrives.  Measured on
-// MI355X, this fine grain keeps
+// (rows x pages) x layers: blockIdx.x walks the rows of a layer's pages, row
+// fastest, and blockIdx.y is the layer, so workgroups dispatched together read
+// (unpack) or write (pack) adjacent rows of the transfer buffer and adjacent
+// rows of each pool page.  A wave splits blockIdx.x into page and row with a
+// shift when a page has a power-of-two number of rows (every common KV page),
+// else with one division.  An unpack wave issues its buffer load before its
+// destination page id arrives.  Measured on MI355X, this fine grain keeps
 // the chip's in-flight accesses within a narrow address window and copies at
 // ~6.6 TB/s, against ~5.6-5.9 TB/s for 8-32 KiB per workgroup, persistent
 // grid-stride loops or ids staged in LDS (a persistent loop serialises each
@@ -50,9 +51,6 @@ constexpr int64_t kTemporalStoreMaxBytes = int64_t(1) << 30;
 // Workgroups per launch stay below 2^25 so that grid * 64 threads fits the
 // 32-bit launch limit with room to spare; larger batches use more launches.
 constexpr int64_t kMaxItemsPerLaunch = int64_t(1) << 25;
-// Pages per launch: the grid's y dimension (a batch with more pages uses
-// more launches).
-constexpr int64_t kMaxPagesPerLaunch = 65535;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -68,6 +66,8 @@ struct CopyParams {
   uint32_t src_pool_pages;
   uint32_t dst_pool_pages;
   uint32_t page_vecs;      // page_bytes / 16
+  uint32_t rows_per_page;  // ceil(page_bytes / kRowBytes)
+  uint32_t rows_log2;      // log2(rows_per_page) when that is a power of two
 };
 
 // Page ids carried in the kernel arguments (small promotions): no device id
@@ -88,18 +88,19 @@ __device__ __forceinline__ void store_vec(const u32x4 v, u32x4* d) {
   else __builtin_nontemporal_store(v, d);
 }
 
-// The copy of one 1 KiB row: row blockIdx.x of page blockIdx.y of layer
-// blockIdx.z (the grid is exactly rows x pages x layers, dispatched row
-// fastest).  sids / dids are the sides' page ids (device or kernel-argument
-// arrays), nullptr for a contiguous side.  Loads are always nontemporal;
-// TEMPORAL selects plain stores (kept in the memory-side cache) instead of
-// nontemporal ones.
-template <bool GUARD, bool TEMPORAL>
+// The copy of one 1 KiB row: item blockIdx.x (page j, row r of it) of layer
+// blockIdx.y; the grid is exactly (rows x pages) x layers.  POW2: the page has
+// a power-of-two number of rows.  sids / dids are the sides' page ids (device
+// or kernel-argument arrays), nullptr for a contiguous side.  Loads are
+// always nontemporal; TEMPORAL selects plain stores (kept in the memory-side
+// cache) instead of nontemporal ones.
+template <bool GUARD, bool TEMPORAL, bool POW2>
 __device__ __forceinline__ void copy_row(const CopyParams& p, const int32_t* sids,
                                          const int32_t* dids) {
-  const uint32_t row = blockIdx.x;
-  const uint32_t j = blockIdx.y;
-  const uint32_t layer = blockIdx.z;
+  const uint32_t x = blockIdx.x;
+  const uint32_t j = POW2 ? x >> p.rows_log2 : x / p.rows_per_page;
+  const uint32_t row = POW2 ? x & (p.rows_per_page - 1) : x - j * p.rows_per_page;
+  const uint32_t layer = blockIdx.y;
   const uint32_t vec = row * kThreads + threadIdx.x;
   // Lane 0 of row 0 is never guarded out, so a skipped tile is still counted.
   if (GUARD && vec >= p.page_vecs) return;
@@ -130,53 +131,62 @@ __device__ __forceinline__ void copy_row(const CopyParams& p, const int32_t* sid
 
 // GUARD: page_bytes is not a multiple of kRowBytes, so the last row of a page
 // is partial.
-template <bool GUARD, bool TEMPORAL>
+template <bool GUARD, bool TEMPORAL, bool POW2>
 __global__ __launch_bounds__(kThreads) void page_copy_kernel(const CopyParams p) {
-  copy_row<GUARD, TEMPORAL>(p, p.src_ids, p.dst_ids);
+  copy_row<GUARD, TEMPORAL, POW2>(p, p.src_ids, p.dst_ids);
 }
 
 // Same copy with the ids in the kernel arguments.  A side whose ids are not
 // inline (the contiguous buffer of a pack or unpack) indexes pages by
 // position.
-template <bool GUARD, bool TEMPORAL, bool SRC_INLINE, bool DST_INLINE>
+template <bool GUARD, bool TEMPORAL, bool POW2, bool SRC_INLINE, bool DST_INLINE>
 __global__ __launch_bounds__(kThreads) void page_copy_inline_kernel(const CopyParamsInline p) {
-  copy_row<GUARD, TEMPORAL>(p.base, SRC_INLINE ? p.src_ids : nullptr, DST_INLINE ? p.dst_ids : nullptr);
+  copy_row<GUARD, TEMPORAL, POW2>(p.base, SRC_INLINE ? p.src_ids : nullptr,
+                                  DST_INLINE ? p.dst_ids : nullptr);
 }
 
-template <bool GUARD, bool TEMPORAL>
+template <bool GUARD, bool TEMPORAL, bool POW2>
 hipError_t launch_t(const CopyParams& p, dim3 grid, hipStream_t stream) {
   void* args[] = {const_cast<CopyParams*>(&p)};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&page_copy_kernel<GUARD, TEMPORAL>), grid,
+  return hipLaunchKernel(reinterpret_cast<const void*>(&page_copy_kernel<GUARD, TEMPORAL, POW2>), grid,
                          dim3(kThreads), args, 0, stream);
 }
 
-hipError_t launch(const CopyParams& p, dim3 grid, bool guard, bool temporal, hipStream_t stream) {
-  if (guard) return temporal ? launch_t<true, true>(p, grid, stream) : launch_t<true, false>(p, grid, stream);
-  return temporal ? launch_t<false, true>(p, grid, stream) : launch_t<false, false>(p, grid, stream);
-}
+// Inline ids on both sides (move), the source only (pack) or the destination
+// only (unpack).
+enum InlineSides { kBothInline = 0, kSrcInline = 1, kDstInline = 2 };
 
-template <bool GUARD, bool TEMPORAL, bool S, bool D>
+template <bool GUARD, bool TEMPORAL, bool POW2, int SIDES>
 hipError_t launch_inline_t(const CopyParamsInline& p, dim3 grid, hipStream_t stream) {
   void* args[] = {const_cast<CopyParamsInline*>(&p)};
+  constexpr bool kS = SIDES != kDstInline, kD = SIDES != kSrcInline;
   return hipLaunchKernel(
-      reinterpret_cast<const void*>(&page_copy_inline_kernel<GUARD, TEMPORAL, S, D>), grid,
+      reinterpret_cast<const void*>(&page_copy_inline_kernel<GUARD, TEMPORAL, POW2, kS, kD>), grid,
       dim3(kThreads), args, 0, stream);
 }
 
-template <bool GUARD, bool TEMPORAL>
-hipError_t launch_inline_g(const CopyParamsInline& p, dim3 grid, bool s, bool d, hipStream_t stream) {
-  if (s && d) return launch_inline_t<GUARD, TEMPORAL, true, true>(p, grid, stream);
-  if (s) return launch_inline_t<GUARD, TEMPORAL, true, false>(p, grid, stream);
-  return launch_inline_t<GUARD, TEMPORAL, false, true>(p, grid, stream);
-}
+using LaunchFn = hipError_t (*)(const CopyParams&, dim3, hipStream_t);
+using LaunchInlineFn = hipError_t (*)(const CopyParamsInline&, dim3, hipStream_t);
 
-hipError_t launch_inline(const CopyParamsInline& p, dim3 grid, bool guard, bool temporal, bool s,
-                         bool d, hipStream_t stream) {
-  if (guard)
-    return temporal ? launch_inline_g<true, true>(p, grid, s, d, stream)
-                    : launch_inline_g<true, false>(p, grid, s, d, stream);
-  return temporal ? launch_inline_g<false, true>(p, grid, s, d, stream)
-                  : launch_inline_g<false, false>(p, grid, s, d, stream);
+// Instances indexed [GUARD][TEMPORAL][POW2] (and [SIDES] for inline ids).
+constexpr LaunchFn kLaunch[2][2][2] = {
+    {{launch_t<false, false, false>, launch_t<false, false, true>},
+     {launch_t<false, true, false>, launch_t<false, true, true>}},
+    {{launch_t<true, false, false>, launch_t<true, false, true>},
+     {launch_t<true, true, false>, launch_t<true, true, true>}}};
+
+template <bool GUARD, bool TEMPORAL, bool POW2>
+constexpr LaunchInlineFn kInlineSides[3] = {launch_inline_t<GUARD, TEMPORAL, POW2, kBothInline>,
+                                            launch_inline_t<GUARD, TEMPORAL, POW2, kSrcInline>,
+                                            launch_inline_t<GUARD, TEMPORAL, POW2, kDstInline>};
+
+LaunchInlineFn launch_inline_fn(bool guard, bool temporal, bool pow2, int sides) {
+  if (guard) {
+    if (temporal) return pow2 ? kInlineSides<true, true, true>[sides] : kInlineSides<true, true, false>[sides];
+    return pow2 ? kInlineSides<true, false, true>[sides] : kInlineSides<true, false, false>[sides];
+  }
+  if (temporal) return pow2 ? kInlineSides<false, true, true>[sides] : kInlineSides<false, true, false>[sides];
+  return pow2 ? kInlineSides<false, false, true>[sides] : kInlineSides<false, false, false>[sides];
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -254,10 +264,13 @@ int launch_page_copy(const Side& src, const Side& dst, int num_layers, int64_t n
     return pages > INT32_MAX ? static_cast<uint32_t>(INT32_MAX) : static_cast<uint32_t>(pages);
   };
 
+  uint32_t rows_log2 = 0;
+  while ((int64_t(1) << rows_log2) < rows_per_page) ++rows_log2;
+  const bool pow2 = (int64_t(1) << rows_log2) == rows_per_page;
+
   for (int l0 = 0; l0 < num_layers; l0 += kMaxLayers) {
     const int nl = num_layers - l0 < kMaxLayers ? num_layers - l0 : kMaxLayers;
-    int64_t max_pages = kMaxItemsPerLaunch / (int64_t(nl) * rows_per_page);
-    if (max_pages > kMaxPagesPerLaunch) max_pages = kMaxPagesPerLaunch;
+    const int64_t max_pages = kMaxItemsPerLaunch / (int64_t(nl) * rows_per_page);
     if (max_pages < 1)
       return fail(PACE_KV_ERANGE, "page_bytes too large for one launch (%lld)", (long long)page_bytes);
     for (int64_t j0 = 0; j0 < n_pages; j0 += max_pages) {
@@ -275,8 +288,9 @@ int launch_page_copy(const Side& src, const Side& dst, int num_layers, int64_t n
       p.src_pool_pages = src_indexed ? clamp_pool(src.pool_pages) : static_cast<uint32_t>(nj);
       p.dst_pool_pages = dst_indexed ? clamp_pool(dst.pool_pages) : static_cast<uint32_t>(nj);
       p.page_vecs = static_cast<uint32_t>(page_bytes / kVecBytes);
-      const dim3 grid(static_cast<uint32_t>(rows_per_page), static_cast<uint32_t>(nj),
-                      static_cast<uint32_t>(nl));
+      p.rows_per_page = static_cast<uint32_t>(rows_per_page);
+      p.rows_log2 = rows_log2;
+      const dim3 grid(static_cast<uint32_t>(rows_per_page * nj), static_cast<uint32_t>(nl));
       const bool temporal = policy == StorePolicy::kTemporalIfSmall &&
                             int64_t(nl) * nj * page_bytes <= kTemporalStoreMaxBytes;
       if (inline_ids) {
@@ -284,11 +298,10 @@ int launch_page_copy(const Side& src, const Side& dst, int num_layers, int64_t n
         q.base = p;
         if (host_src_ids) memcpy(q.src_ids, host_src_ids + j0, nj * sizeof(int32_t));
         if (host_dst_ids) memcpy(q.dst_ids, host_dst_ids + j0, nj * sizeof(int32_t));
-        rc = hip_status(launch_inline(q, grid, guard, temporal, host_src_ids != nullptr,
-                                      host_dst_ids != nullptr, stream),
-                        "page copy launch");
+        const int sides = host_src_ids && host_dst_ids ? kBothInline : (host_src_ids ? kSrcInline : kDstInline);
+        rc = hip_status(launch_inline_fn(guard, temporal, pow2, sides)(q, grid, stream), "page copy launch");
       } else {
-        rc = hip_status(launch(p, grid, guard, temporal, stream), "page copy launch");
+        rc = hip_status(kLaunch[guard][temporal][pow2](p, grid, stream), "page copy launch");
       }
       if (rc) return rc;
     }

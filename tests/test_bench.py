@@ -12,8 +12,8 @@ import pytest
 import bench
 
 ROOT = Path(__file__).resolve().parent.parent
-COPY = "void pace_kv::(anonymous namespace)::page_copy_kernel<false, false>(pace_kv::(anonymous namespace)::CopyParams)"
-COPY_T = COPY.replace("<false, false>", "<false, true>")
+COPY = "void pace_kv::(anonymous namespace)::page_copy_kernel<false, false, true>(pace_kv::(anonymous namespace)::CopyParams)"
+COPY_T = COPY.replace("<false, false, true>", "<false, true, true>")
 
 
 def write_csv(path, rows):
@@ -27,11 +27,13 @@ def write_csv(path, rows):
 def test_copy_kernel_names_follow_the_store_policy():
     big = bench.TEMPORAL_STORE_MAX_BYTES + 1
     assert bench.copy_kernel_names("buffer", big, 65536) == \
-        "page_copy_kernel<false, false> (pack and unpack, nontemporal stores)"
+        "page_copy_kernel<false, false, true> (pack and unpack, nontemporal stores)"
     small = bench.copy_kernel_names("buffer", 64 << 20, 65536)
-    assert "page_copy_kernel<false, true> (pack, plain stores)" in small
-    assert "page_copy_kernel<false, false> (unpack" in small
-    assert bench.copy_kernel_names("fused", 64 << 20, 96).startswith("page_copy_kernel<true, false> (move")
+    assert "page_copy_kernel<false, true, true> (pack, plain stores)" in small
+    assert "page_copy_kernel<false, false, true> (unpack" in small
+    # 96 B: one partial row (a power of two); 3 KiB: three rows (not)
+    assert bench.copy_kernel_names("fused", 64 << 20, 96).startswith("page_copy_kernel<true, false, true> (move")
+    assert bench.copy_kernel_names("fused", 64 << 20, 3072).startswith("page_copy_kernel<false, false, false>")
 
 
 def test_summarize_pmc_scales_counters_by_the_calibration_copy(tmp_path):
@@ -51,7 +53,7 @@ def test_summarize_pmc_scales_counters_by_the_calibration_copy(tmp_path):
     assert d["write_bytes_per_launch"] == 2000 * 1024
     assert d["traffic_bytes_per_launch"] == 4000 * 1024
     assert d["fetch_dispatches"] == 2
-    assert d["kernel"] == "page_copy_kernel<false, false> and page_copy_kernel<false, true>"
+    assert d["kernel"] == "page_copy_kernel<false, false, true> and page_copy_kernel<false, true, true>"
 
 
 def test_summarize_pmc_needs_both_kinds_of_dispatch(tmp_path):
@@ -66,7 +68,7 @@ def test_pmc_markdown_states_algorithmic_bytes_per_layer_chunk(tmp_path):
 
     w = workloads.get("llama3-70b-256req-bf16")
     alg = 2 * 8 * w.n_pages * w.shape.page_bytes          # one launch = one 8-layer chunk
-    t = {"workload": "llama3-70b-256req-bf16", "kernel": "page_copy_kernel<false, false>",
+    t = {"workload": "llama3-70b-256req-bf16", "kernel": "page_copy_kernel<false, false, true>",
          "fetch_kib_per_dispatch_raw": 1.0, "fetch_calibration_kib_raw": 2.0, "fetch_scale": 2.0,
          "fetch_bytes_per_launch": alg // 2, "fetch_dispatches": 3, "write_kib_per_dispatch_raw": 1.0,
          "write_calibration_kib_raw": 1.0, "write_scale": 1.0, "write_bytes_per_launch": alg // 2,

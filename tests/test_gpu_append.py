@@ -121,3 +121,32 @@ def test_partially_prefilled_request_promoted_then_continued(gpu):
     torch.cuda.synchronize()
     for l in range(L):
         assert torch.equal(words(hp[l]), words(ref[l])), f"layer {l}"
+
+
+def test_append_of_70000_tokens(gpu):
+    # 70 000 tokens of two requests (one prefill, one continued) in one launch
+    # of 140 000 workgroups.
+    P, H, D, pages = 16, 1, 8, 5000
+    g = torch.Generator(device=gpu).manual_seed(31)
+    cache = torch.randn((pages, 2, P, H, D), generator=g, device=gpu).half()
+    seq_lens = [60000, 10005]                 # request 1 already held 5 tokens
+    new = [60000, 10000]
+    npages = [-(-n // P) for n in seq_lens]
+    kv_indptr = i32([0, npages[0], npages[0] + npages[1]], gpu)
+    kv_indices = torch.randperm(pages, generator=torch.Generator().manual_seed(32))[:sum(npages)].to(torch.int32).to(gpu)
+    last = i32([n - (k - 1) * P for n, k in zip(seq_lens, npages)], gpu)
+    append_indptr = i32([0, new[0], new[0] + new[1]], gpu)
+    nnz = sum(new)
+    key = torch.randn((nnz, H, D), generator=g, device=gpu).half()
+    value = torch.randn((nnz, H, D), generator=g, device=gpu).half()
+    bi, pos = ap.get_batch_indices_positions(append_indptr, ap.get_seq_lens(kv_indptr, last, P), nnz)
+    before = cache.clone()
+    ap.append_paged_kv_cache(key, value, bi, pos, cache, kv_indices, kv_indptr, last)
+    torch.cuda.synchronize()
+    b_l, p_l = bi.long(), pos.long()
+    page_t = kv_indices.long()[kv_indptr.long()[b_l] + p_l // P]
+    assert torch.equal(words(cache[page_t, 0, p_l % P]), words(key))
+    assert torch.equal(words(cache[page_t, 1, p_l % P]), words(value))
+    # the 5 tokens request 1 held before the append are untouched
+    first = kv_indices.long()[npages[0]]
+    assert torch.equal(words(cache[first, :, :5]), words(before[first, :, :5]))

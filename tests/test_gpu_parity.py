@@ -156,13 +156,10 @@ def test_out_of_range_ids_are_skipped_and_counted(gpu):
         assert same(dst[l][keep], before[l][keep])
 
 
-def test_batches_over_65535_pages_split_across_launches(gpu):
-    # 128-byte pages (a partial 1 KiB row each): 131 073 pages take three
-    # launches per layer chunk on the grid's page dimension.
-    L, pages, shape, n = 2, 140_000, (2, 4, 1, 8), 131_073
-    src = rand_pool(L, pages, shape, torch.float16, gpu, 11)
-    dst = rand_pool(L, pages, shape, torch.float16, gpu, 12)
-    g = torch.Generator(device=gpu).manual_seed(13)
+def check_large_batch(gpu, L, pages, shape, n, seed):
+    src = rand_pool(L, pages, shape, torch.float16, gpu, seed)
+    dst = rand_pool(L, pages, shape, torch.float16, gpu, seed + 1)
+    g = torch.Generator(device=gpu).manual_seed(seed + 2)
     s_ids = torch.randperm(pages, generator=g, device=gpu)[:n].to(torch.int32)
     d_ids = torch.randperm(pages, generator=g, device=gpu)[:n].to(torch.int32)
     want = [d.clone() for d in dst]
@@ -176,6 +173,19 @@ def test_batches_over_65535_pages_split_across_launches(gpu):
     for l in range(L):
         assert same(buf[l], src[l].index_select(0, s_ids.long()))
         assert same(dst[l], want[l]) and same(fused[l], want[l])
+
+
+def test_batches_of_more_than_65535_pages(gpu):
+    # 128-byte pages (a partial 1 KiB row each): 131 073 pages in one launch
+    # of 131 073 x 2 workgroups.
+    check_large_batch(gpu, 2, 140_000, (2, 4, 1, 8), 131_073, 11)
+
+
+def test_batches_over_2_pow_25_workgroups_split_across_launches(gpu):
+    # 16-byte pages (one workgroup each): 2^24 + 7 pages of 2 layers are
+    # 2^25 + 14 workgroups, more than one launch takes, so the pages split
+    # over two launches.
+    check_large_batch(gpu, 2, (1 << 24) + 100, (2, 1, 1, 4), (1 << 24) + 7, 21)
 
 
 def test_empty_batch_is_a_no_op(gpu):
