@@ -787,14 +787,21 @@ def summarize_stats(stats_csv: str, bench_json: str, command: str, trace_csv: st
            f"payload {cfg['payload_bytes']} B.", "", "Command (repo root, one MI355X):", "", "```",
            "export TMPDIR=/tmp", command, "```", "",
            "| kernel | calls | average ns | min ns | max ns | std dev ns |", "|---|---|---|---|---|---|"]
-    for r in rows:
+    ours = [r for r in rows if "pace_kv::" in r["Name"]]
+    others = sorted((r for r in rows if "pace_kv::" not in r["Name"]),
+                    key=lambda r: -float(r["TotalDurationNs"]))
+    for r in ours + others[:4]:
         name = r["Name"]
-        if "pace_kv" in name:
-            short = name.replace("void pace_kv::(anonymous namespace)::", "").split("(")[0]
+        if "pace_kv::" in name:
+            short = name.split("(anonymous namespace)::", 1)[-1].split("(")[0]
         else:
             short = "torch normal_ (pool fill)" if "distribution" in name else name[:48]
         out.append(f"| {short} | {r['Calls']} | {float(r['AverageNs']):.0f} | {r['MinNs']} | {r['MaxNs']} | "
                    f"{float(r['StdDev']):.0f} |")
+    if others[4:]:
+        rest = others[4:]
+        out.append(f"| {len(rest)} more kernels (torch: checks, baselines, set-up) | "
+                   f"{sum(int(r['Calls']) for r in rest)} | | | | |")
     pc = [r for r in rows if "page_copy_kernel" in r["Name"]]
     if pc:
         calls = sum(int(r["Calls"]) for r in pc)
@@ -872,7 +879,8 @@ def pmc_markdown(traffic_json: str) -> str:
     # one launch reads and writes its layer chunk's pages once
     chunk = min(w.device_layers_per_chunk or w.shape.num_layers, w.shape.num_layers)
     alg = 2 * chunk * w.n_pages * w.shape.page_bytes
-    run = f"python3 bench.py --workload {wl} --no-cpu --no-promote --no-staging --steps 3 --warmup 1 --calibrate"
+    run = (f"python3 bench.py --workload {wl} --no-cpu --no-promote --no-staging --no-dropin --no-append "
+           "--steps 3 --warmup 1 --calibrate")
     cmds = [
         "export TMPDIR=/tmp",
         f"timeout -s KILL 300 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch_{wl} -o f -- {run}",
