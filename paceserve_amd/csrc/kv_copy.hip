@@ -391,7 +391,8 @@ int pace_kv_pack(const void* const* src_layers, int num_layers, int64_t pool_pag
   if (num_layers < 0) return fail(PACE_KV_EINVAL, "num_layers must be >= 0");
   if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
   if (page_ids == nullptr || out == nullptr) return fail(PACE_KV_EINVAL, "pack: NULL page_ids or out");
-  if (n_pages > 0 && page_bytes > 0 && out_layer_stride < n_pages * page_bytes)
+  if (n_pages > 0 && page_bytes > 0 &&
+      (n_pages > INT64_MAX / page_bytes || out_layer_stride < n_pages * page_bytes))
     return fail(PACE_KV_ERANGE, "pack: out_layer_stride %lld < n_pages*page_bytes",
                 (long long)out_layer_stride);
   if (out_layer_stride % 16 != 0) return fail(PACE_KV_EINVAL, "pack: out_layer_stride not a multiple of 16");
@@ -410,7 +411,8 @@ int pace_kv_unpack(const void* buf, int64_t buf_layer_stride, void* const* dst_l
   if (num_layers < 0) return fail(PACE_KV_EINVAL, "num_layers must be >= 0");
   if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
   if (page_ids == nullptr || buf == nullptr) return fail(PACE_KV_EINVAL, "unpack: NULL page_ids or buf");
-  if (n_pages > 0 && page_bytes > 0 && buf_layer_stride < n_pages * page_bytes)
+  if (n_pages > 0 && page_bytes > 0 &&
+      (n_pages > INT64_MAX / page_bytes || buf_layer_stride < n_pages * page_bytes))
     return fail(PACE_KV_ERANGE, "unpack: buf_layer_stride %lld < n_pages*page_bytes",
                 (long long)buf_layer_stride);
   if (buf_layer_stride % 16 != 0) return fail(PACE_KV_EINVAL, "unpack: buf_layer_stride not a multiple of 16");

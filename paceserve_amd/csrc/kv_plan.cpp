@@ -345,7 +345,8 @@ int pace_kv_promote(pace_kv_promoter* pr, pace_kv_allocator* dst_alloc,
     return fail(PACE_KV_EINVAL, "page_bytes must be a positive multiple of 16");
   if (num_layers > 0 && (src_layers == nullptr || dst_layers == nullptr))
     return fail(PACE_KV_EINVAL, "promote: NULL layer table");
-  if (buffer != nullptr && (buffer_layer_stride < n * page_bytes || buffer_layer_stride % 16 != 0))
+  if (buffer != nullptr && (n > INT64_MAX / page_bytes || buffer_layer_stride < n * page_bytes ||
+                            buffer_layer_stride % 16 != 0))
     return fail(PACE_KV_ERANGE, "promote: buffer_layer_stride must be >= n_pages*page_bytes and a multiple of 16");
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (n <= PACE_KV_INLINE_IDS) return promote_inline(pr, dst_alloc, src_layers, src_pool_pages,
