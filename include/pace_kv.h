@@ -50,7 +50,9 @@ enum pace_kv_status {
   PACE_KV_EINVAL = -1,   /* null pointer, negative size, misalignment        */
   PACE_KV_ERANGE = -2,   /* page id or size outside what a buffer holds      */
   PACE_KV_ENOMEM = -3,   /* allocator exhausted (no free pages)              */
-  PACE_KV_ESTATE = -4    /* object used in a state that does not allow it    */
+  PACE_KV_ESTATE = -4,   /* object used in a state that does not allow it    */
+  PACE_KV_ETIMEDOUT = -5, /* a channel wait passed its deadline               */
+  PACE_KV_ECLOSED = -6   /* the channel was closed by either side            */
 };
 
 /* ABI version this library was built with (PACE_KV_ABI_VERSION). */
@@ -337,6 +339,101 @@ int pace_kv_promote(pace_kv_promoter* promoter, pace_kv_allocator* dst_alloc,
                     const int32_t* dst_pages, void* buffer,
                     int64_t buffer_layer_stride, int buffer_layers,
                     int32_t* out_dst_tables, int32_t* err_count, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Cross-process channel                                                     */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * A named shared-memory ring (POSIX shm "/<name>") that carries packed KV
+ * pages from a sender process to a receiver process, with no serialization
+ * and no object store: the sender packs a layer chunk, copies it to pinned
+ * memory and from there into a ring slot (a pool of copy_threads host threads
+ * does that copy); the receiver copies a slot out to pinned memory, uploads
+ * it and unpacks it, chunk by chunk, overlapped.  A message is a header (its
+ * shape and an opaque metadata blob of at most slot_bytes, e.g. the sequence
+ * id and source block table) followed by its payload in the transfer-buffer
+ * layout [num_layers][n_pages][page_bytes], in chunks of whole layers when a
+ * layer fits in a slot, else of pages of one layer (a page must fit).
+ * Messages larger than the ring stream through it, so the receiver must be
+ * receiving while the sender sends.
+ *
+ * One sender and one receiver per channel; each endpoint serialises its own
+ * sends (whole messages) and its own receives.  Every blocking call waits at
+ * most timeout_ms milliseconds (PACE_KV_ETIMEDOUT; 0 = do not wait) and
+ * returns PACE_KV_ECLOSED once either side has closed the channel.  A sender
+ * that fails after the header marks the message abandoned, and the
+ * receiver's next wait for its chunks fails with PACE_KV_ESTATE.
+ *
+ * Replaces the transfer of a KVobj from a prefill instance to a decode
+ * instance through Ray's object store (paceserve/disutil/prefill_instance.py:
+ * 96-107 transfer_kv_cache returns the KVobj holding the host tensor;
+ * paceserve/disutil/decode_instance.py:165-171 ray.get()s it and inserts it;
+ * paceserve/core/datatypes/kv_cache_obj.py:7-21 KVobj): only the sequence id
+ * crosses the control plane, the pages cross the ring.
+ */
+typedef struct pace_kv_channel pace_kv_channel;
+
+/* Creates the channel "/<name>" (fails with PACE_KV_ESTATE if it exists):
+ * num_slots in [2, 64] slots of slot_bytes (a multiple of 4096).  The
+ * creator's close unlinks the name.  copy_threads in [1, 64]. */
+int pace_kv_channel_create(const char* name, int64_t slot_bytes, int num_slots,
+                           int copy_threads, pace_kv_channel** out);
+/* Opens a channel created by the peer, waiting up to timeout_ms for it. */
+int pace_kv_channel_open(const char* name, int copy_threads, int timeout_ms,
+                         pace_kv_channel** out);
+/* Marks the channel closed for both sides, waits for this endpoint's device
+ * work, and unmaps it.  No call may be in progress on this endpoint. */
+int pace_kv_channel_close(pace_kv_channel* channel);
+int pace_kv_channel_info(pace_kv_channel* channel, int64_t* slot_bytes,
+                         int* num_slots);
+
+/* Sends one message whose payload is packed from device pools:
+ *   payload[l][j] = src_layers[l][page_ids[j]] (page_ids: device int32).
+ * Packs run on `stream` after its earlier work.  Returns once every chunk is
+ * in the ring (host-synchronous); *msg_id receives the message's id. */
+int pace_kv_channel_send(pace_kv_channel* channel,
+                         const void* const* src_layers, int num_layers,
+                         int64_t pool_pages, const int32_t* page_ids,
+                         int64_t n_pages, int64_t page_bytes,
+                         const void* meta, int64_t meta_bytes, int timeout_ms,
+                         uint64_t* msg_id, void* stream);
+/* Sends one message whose payload is already in host memory, contiguous in
+ * the transfer-buffer layout (num_layers * n_pages * page_bytes bytes). */
+int pace_kv_channel_send_host(pace_kv_channel* channel, const void* payload,
+                              int num_layers, int64_t n_pages,
+                              int64_t page_bytes, const void* meta,
+                              int64_t meta_bytes, int timeout_ms,
+                              uint64_t* msg_id);
+
+/* Receives the next message's header: its metadata (into meta, meta_cap
+ * bytes; with a smaller buffer PACE_KV_ERANGE reports the size in
+ * *meta_bytes and leaves the message in place) and its shape.  The payload
+ * must then be received (pace_kv_channel_recv or _recv_host) before the next
+ * header; a header with num_layers or n_pages 0 has none. */
+int pace_kv_channel_recv_header(pace_kv_channel* channel, void* meta,
+                                int64_t meta_cap, int64_t* meta_bytes,
+                                int* num_layers, int64_t* n_pages,
+                                int64_t* page_bytes, uint64_t* msg_id,
+                                int timeout_ms);
+/* Receives the current message's payload into device pools:
+ *   dst_layers[l][page_ids[j]] = payload[l][j] (page_ids: device int32,
+ * distinct).  The shape must equal the header's.  Unpacks run on `stream`
+ * after its earlier work; the call returns once every chunk has left the
+ * ring, with the last unpacks still enqueued.  Ids outside [0, pool_pages)
+ * are skipped and counted in err_count, as in pace_kv_unpack.  After a
+ * PACE_KV_ETIMEDOUT the call may be repeated and continues where it
+ * stopped. */
+int pace_kv_channel_recv(pace_kv_channel* channel, void* const* dst_layers,
+                         int num_layers, int64_t pool_pages,
+                         const int32_t* page_ids, int64_t n_pages,
+                         int64_t page_bytes, int32_t* err_count,
+                         int timeout_ms, void* stream);
+/* Receives the current message's payload into host memory (payload_bytes
+ * must equal the payload's size), or discards it when payload is NULL (a
+ * receiver that cannot take the message must still drain it). */
+int pace_kv_channel_recv_host(pace_kv_channel* channel, void* payload,
+                              int64_t payload_bytes, int timeout_ms);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
-from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_void_p
+from ctypes import POINTER, c_char_p, c_int, c_int32, c_int64, c_uint64, c_void_p
 from pathlib import Path
 
 import torch  # noqa: F401  (binds the HIP runtime before the library loads)
@@ -24,6 +24,8 @@ PACE_KV_EINVAL = -1
 PACE_KV_ERANGE = -2
 PACE_KV_ENOMEM = -3
 PACE_KV_ESTATE = -4
+PACE_KV_ETIMEDOUT = -5
+PACE_KV_ECLOSED = -6
 
 # name -> (restype, argtypes); mirrors include/pace_kv.h.
 _VP = c_void_p
@@ -59,6 +61,20 @@ SIGNATURES = {
         c_int,
         [_VP, _VP, _VP, c_int64, _VP, c_int64, c_int, c_int64, c_int, _VP, _VP, _VP, _VP, c_int64,
          c_int, _VP, _VP, _VP]),
+    "pace_kv_channel_create": (c_int, [c_char_p, c_int64, c_int, c_int, POINTER(c_void_p)]),
+    "pace_kv_channel_open": (c_int, [c_char_p, c_int, c_int, POINTER(c_void_p)]),
+    "pace_kv_channel_close": (c_int, [_VP]),
+    "pace_kv_channel_info": (c_int, [_VP, POINTER(c_int64), POINTER(c_int)]),
+    "pace_kv_channel_send": (
+        c_int, [_VP, _VP, c_int, c_int64, _VP, c_int64, c_int64, _VP, c_int64, c_int, POINTER(c_uint64), _VP]),
+    "pace_kv_channel_send_host": (
+        c_int, [_VP, _VP, c_int, c_int64, c_int64, _VP, c_int64, c_int, POINTER(c_uint64)]),
+    "pace_kv_channel_recv_header": (
+        c_int, [_VP, _VP, c_int64, POINTER(c_int64), POINTER(c_int), POINTER(c_int64), POINTER(c_int64),
+                POINTER(c_uint64), c_int]),
+    "pace_kv_channel_recv": (
+        c_int, [_VP, _VP, c_int, c_int64, _VP, c_int64, c_int64, _VP, c_int, _VP]),
+    "pace_kv_channel_recv_host": (c_int, [_VP, _VP, c_int64, c_int]),
     "pace_kv_roundtrip": (
         c_int,
         [_VP, _VP, c_int64, _VP, _VP, c_int64, _VP, c_int, c_int64, c_int64, c_int, _VP, c_int64,

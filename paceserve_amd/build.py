@@ -19,7 +19,7 @@ INCLUDE_DIR = REPO_DIR / "include"
 LIB_NAME = "libpace_kv.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 
-SOURCES = ["kv_copy.hip", "kv_stage.hip", "kv_plan.cpp", "kv_append.hip"]
+SOURCES = ["kv_copy.hip", "kv_stage.hip", "kv_plan.cpp", "kv_append.hip", "kv_channel.cpp"]
 HEADERS = ["internal.h"]
 
 # Packed-FP32 instructions are disabled for every HIP translation unit.

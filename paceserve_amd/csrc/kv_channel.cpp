@@ -1,0 +1,815 @@
+// Cross-process KV channel: moves packed KV pages from one process to
+// another through a named shared-memory ring, in place of pickling the host
+// tensor through an object store.
+//
+// Layout of the shared object (POSIX shm, /dev/shm/<name>):
+//   ChannelCtl (control block: ring counters, per-slot records)
+//   num_slots data slots of slot_bytes each, page-aligned
+// One sender and one receiver (single producer, single consumer).  The sender
+// owns `head` (slots published), the receiver owns `tail` (slots released);
+// both are 32-bit futex words, compared modulo 2^32.  A slot holds one record:
+// a message header (shape + an opaque metadata blob) or one chunk of the
+// message's payload.  The payload is the contiguous transfer-buffer layout
+// [num_layers][n_pages][page_bytes]; a chunk is a run of whole layers when a
+// layer fits in a slot, else a run of pages of one layer.
+//
+// The device legs stage through pinned memory, since a kernel or DMA engine
+// cannot reach the shared mapping (it is pageable; pinning memory that already
+// exists is not available): the sender packs chunk c into a device slot,
+// copies it to a pinned slot, and copies that into the shared slot with a pool
+// of host threads while chunk c+1 is packed and copied down; the receiver
+// copies a shared slot into a pinned slot (releasing the shared slot at once),
+// then uploads it and unpacks it while the next chunk is copied.
+#include <errno.h>
+#include <fcntl.h>
+#include <linux/futex.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <sys/syscall.h>
+#include <time.h>
+#include <unistd.h>
+
+#include <atomic>
+#include <chrono>
+#include <condition_variable>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "internal.h"
+
+using pace_kv::fail;
+using pace_kv::hip_status;
+
+namespace {
+
+constexpr uint64_t kMagic = 0x50414345'4b564348ull;  // "PACEKVCH"
+constexpr uint32_t kVersion = 1;
+constexpr int kMaxSlots = 64;
+constexpr int kNameMax = 200;
+
+enum RecordKind : uint32_t { kEmpty = 0, kHeader = 1, kData = 2 };
+
+static_assert(sizeof(std::atomic<uint32_t>) == 4, "futex words are 32-bit");
+static_assert(std::atomic<uint32_t>::is_always_lock_free, "shared counters must be lock-free");
+static_assert(std::atomic<uint64_t>::is_always_lock_free, "shared counters must be lock-free");
+
+struct alignas(64) SlotRecord {
+  uint32_t kind;
+  uint32_t chunk;        // data: chunk index within the message
+  uint64_t msg_id;
+  int64_t offset;        // data: byte offset of the chunk in the payload
+  int64_t bytes;         // data: chunk bytes; header: metadata bytes
+  int64_t n_pages;       // header
+  int64_t page_bytes;    // header
+  int32_t num_layers;    // header
+  int32_t pad;
+};
+
+struct alignas(64) ChannelCtl {
+  uint64_t magic;
+  uint32_t version;
+  uint32_t num_slots;
+  int64_t slot_bytes;
+  int64_t data_offset;   // first data slot, from the start of the mapping
+  int64_t total_bytes;
+  alignas(64) std::atomic<uint32_t> head;    // sender: records published
+  alignas(64) std::atomic<uint32_t> tail;    // receiver: records released
+  alignas(64) std::atomic<uint32_t> closed;  // either side closed the channel
+  std::atomic<uint64_t> next_msg_id;         // sender: id of the next message
+  std::atomic<uint64_t> aborted_msg;         // sender: id of a message it gave up (0 = none)
+  SlotRecord slots[kMaxSlots];
+};
+
+int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+long futex(std::atomic<uint32_t>* word, int op, uint32_t val, const timespec* ts) {
+  return syscall(SYS_futex, reinterpret_cast<uint32_t*>(word), op, val, ts, nullptr, 0);
+}
+
+void wake_all(std::atomic<uint32_t>* word) { (void)futex(word, FUTEX_WAKE, INT32_MAX, nullptr); }
+
+// Splits large host copies over a pool of threads (the caller takes a share).
+// A job's fields change only while no worker is inside work(): a worker joins
+// a job under the lock (active_), and the caller waits for active_ == 0 both
+// before setting up a job and before returning from it.
+class CopyPool {
+ public:
+  explicit CopyPool(int threads) {
+    for (int i = 1; i < threads; ++i) workers_.emplace_back([this] { run(); });
+  }
+  ~CopyPool() {
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      stop_ = true;
+    }
+    cv_.notify_all();
+    for (auto& t : workers_) t.join();
+  }
+  void copy(void* dst, const void* src, int64_t bytes) {
+    constexpr int64_t kPart = 2 << 20;
+    if (workers_.empty() || bytes <= 2 * kPart) {
+      memcpy(dst, src, static_cast<size_t>(bytes));
+      return;
+    }
+    std::lock_guard<std::mutex> one_job(job_mu_);  // one job at a time
+    std::unique_lock<std::mutex> lock(mu_);
+    done_cv_.wait(lock, [this] { return active_ == 0; });
+    dst_ = static_cast<char*>(dst);
+    src_ = static_cast<const char*>(src);
+    bytes_ = bytes;
+    const int64_t want = static_cast<int64_t>(workers_.size()) + 1;
+    part_ = round_up((bytes + want - 1) / want, 4096);
+    parts_ = (bytes + part_ - 1) / part_;
+    next_.store(0);
+    finished_ = 0;
+    ++generation_;
+    lock.unlock();
+    cv_.notify_all();
+    const int64_t mine = work();
+    lock.lock();
+    finished_ += mine;
+    done_cv_.wait(lock, [this] { return finished_ == parts_ && active_ == 0; });
+  }
+
+ private:
+  int64_t work() {
+    int64_t done = 0;
+    for (;;) {
+      const int64_t i = next_.fetch_add(1);
+      if (i >= parts_) return done;
+      const int64_t off = i * part_;
+      const int64_t n = bytes_ - off < part_ ? bytes_ - off : part_;
+      memcpy(dst_ + off, src_ + off, static_cast<size_t>(n));
+      ++done;
+    }
+  }
+  void run() {
+    uint64_t seen = 0;
+    std::unique_lock<std::mutex> lock(mu_);
+    for (;;) {
+      cv_.wait(lock, [&] { return stop_ || generation_ != seen; });
+      if (stop_) return;
+      seen = generation_;
+      ++active_;
+      lock.unlock();
+      const int64_t mine = work();
+      lock.lock();
+      finished_ += mine;
+      --active_;
+      done_cv_.notify_all();
+    }
+  }
+
+  std::vector<std::thread> workers_;
+  std::mutex job_mu_;
+  std::mutex mu_;
+  std::condition_variable cv_, done_cv_;
+  bool stop_ = false;
+  uint64_t generation_ = 0;
+  int active_ = 0;
+  char* dst_ = nullptr;
+  const char* src_ = nullptr;
+  int64_t bytes_ = 0, part_ = 0, parts_ = 0, finished_ = 0;
+  std::atomic<int64_t> next_{0};
+};
+
+// Chunks of a message: whole layers per chunk when a layer fits in a slot,
+// else runs of pages of one layer.
+struct Chunking {
+  int num_layers = 0;
+  int64_t n_pages = 0, page_bytes = 0, layer_bytes = 0;
+  int layers_per_chunk = 0;     // > 0: layer chunks
+  int64_t pages_per_chunk = 0;  // > 0: page chunks
+  int64_t chunks_per_layer = 0;
+  int64_t num_chunks = 0;
+
+  struct Chunk {
+    int layer, nl;     // first layer and layer count
+    int64_t j0, nj;    // first page and page count (all pages for layer chunks)
+    int64_t offset, bytes;
+  };
+  Chunk at(int64_t c) const {
+    Chunk k;
+    if (layers_per_chunk > 0) {
+      k.layer = static_cast<int>(c * layers_per_chunk);
+      k.nl = num_layers - k.layer < layers_per_chunk ? num_layers - k.layer : layers_per_chunk;
+      k.j0 = 0;
+      k.nj = n_pages;
+      k.offset = k.layer * layer_bytes;
+      k.bytes = k.nl * layer_bytes;
+    } else {
+      k.layer = static_cast<int>(c / chunks_per_layer);
+      k.nl = 1;
+      k.j0 = (c % chunks_per_layer) * pages_per_chunk;
+      k.nj = n_pages - k.j0 < pages_per_chunk ? n_pages - k.j0 : pages_per_chunk;
+      k.offset = k.layer * layer_bytes + k.j0 * page_bytes;
+      k.bytes = k.nj * page_bytes;
+    }
+    return k;
+  }
+};
+
+int make_chunking(int num_layers, int64_t n_pages, int64_t page_bytes, int64_t slot_bytes, Chunking* out) {
+  if (num_layers < 0 || n_pages < 0) return fail(PACE_KV_EINVAL, "channel: negative num_layers or n_pages");
+  if (page_bytes <= 0 || page_bytes % 16 != 0)
+    return fail(PACE_KV_EINVAL, "channel: page_bytes must be a positive multiple of 16");
+  if (page_bytes > slot_bytes)
+    return fail(PACE_KV_ERANGE, "channel: a page (%lld bytes) does not fit a slot (%lld bytes)",
+                (long long)page_bytes, (long long)slot_bytes);
+  if (n_pages > INT64_MAX / page_bytes / (num_layers > 0 ? num_layers : 1))
+    return fail(PACE_KV_ERANGE, "channel: payload size overflows");
+  Chunking& k = *out;
+  k.num_layers = num_layers;
+  k.n_pages = n_pages;
+  k.page_bytes = page_bytes;
+  k.layer_bytes = n_pages * page_bytes;
+  if (num_layers == 0 || n_pages == 0) {
+    k.num_chunks = 0;
+    k.layers_per_chunk = 1;
+    return PACE_KV_OK;
+  }
+  if (k.layer_bytes <= slot_bytes) {
+    const int64_t per = slot_bytes / k.layer_bytes;
+    k.layers_per_chunk = static_cast<int>(per < num_layers ? per : num_layers);
+    k.num_chunks = (num_layers + k.layers_per_chunk - 1) / k.layers_per_chunk;
+  } else {
+    k.layers_per_chunk = 0;
+    k.pages_per_chunk = slot_bytes / page_bytes;
+    k.chunks_per_layer = (n_pages + k.pages_per_chunk - 1) / k.pages_per_chunk;
+    k.num_chunks = k.chunks_per_layer * num_layers;
+  }
+  return PACE_KV_OK;
+}
+
+// Device-side staging of one endpoint: two device slots and two pinned slots
+// of slot_bytes, a copy stream and the events that guard slot reuse.
+struct Staging {
+  int device = -1;
+  char* dev[2] = {nullptr, nullptr};
+  char* pinned[2] = {nullptr, nullptr};
+  hipStream_t copy = nullptr;
+  hipEvent_t filled[2] = {nullptr, nullptr};  // device slot written (pack, or upload)
+  hipEvent_t copied[2] = {nullptr, nullptr};  // copy between device and pinned slot finished
+  hipEvent_t drained[2] = {nullptr, nullptr}; // receiver: unpack of the device slot finished
+  bool ready = false;
+};
+
+}  // namespace
+
+struct pace_kv_channel {
+  std::string name;
+  bool creator = false;
+  int fd = -1;
+  char* base = nullptr;
+  int64_t map_bytes = 0;
+  ChannelCtl* ctl = nullptr;
+  CopyPool* pool = nullptr;
+  std::mutex send_mu;   // one message at a time from this endpoint
+  std::mutex recv_mu;
+  Staging tx, rx;       // device staging of sends and of receives
+  // receiver state of the message in progress
+  bool rx_active = false;
+  uint64_t rx_msg = 0;
+  Chunking rx_chunks;
+  int64_t rx_next = 0;
+};
+
+namespace {
+
+char* slot_data(pace_kv_channel* ch, uint32_t idx) {
+  return ch->base + ch->ctl->data_offset + static_cast<int64_t>(idx) * ch->ctl->slot_bytes;
+}
+
+// Waits until cond() holds.  `word` is the futex word the other side bumps
+// when it may have made cond() true; closing the channel also wakes it.
+template <class Cond>
+int wait_for(pace_kv_channel* ch, std::atomic<uint32_t>* word, Cond cond, int timeout_ms,
+             const char* what) {
+  using clock = std::chrono::steady_clock;
+  const auto deadline = clock::now() + std::chrono::milliseconds(timeout_ms < 0 ? 0 : timeout_ms);
+  for (int spin = 0;; ++spin) {
+    const uint32_t seen = word->load(std::memory_order_acquire);
+    if (cond()) return PACE_KV_OK;
+    if (ch->ctl->closed.load(std::memory_order_acquire))
+      return fail(PACE_KV_ECLOSED, "channel %s: closed while waiting for %s", ch->name.c_str(), what);
+    if (spin < 256) {
+      __builtin_ia32_pause();
+      continue;
+    }
+    const auto left = std::chrono::duration_cast<std::chrono::microseconds>(deadline - clock::now()).count();
+    if (left <= 0)
+      return fail(PACE_KV_ETIMEDOUT, "channel %s: timed out after %d ms waiting for %s", ch->name.c_str(),
+                  timeout_ms, what);
+    const long us = left < 10000 ? left : 10000;
+    timespec ts{us / 1000000, (us % 1000000) * 1000};
+    (void)futex(word, FUTEX_WAIT, seen, &ts);
+  }
+}
+
+// Sender: waits for a free slot and returns its index.
+int acquire_slot(pace_kv_channel* ch, int timeout_ms, uint32_t* idx) {
+  ChannelCtl* c = ch->ctl;
+  const uint32_t h = c->head.load(std::memory_order_relaxed);
+  PACE_KV_TRY(wait_for(ch, &c->tail,
+                       [&] { return h - c->tail.load(std::memory_order_acquire) < c->num_slots; },
+                       timeout_ms, "a free slot"));
+  *idx = h % c->num_slots;
+  return PACE_KV_OK;
+}
+
+void publish(pace_kv_channel* ch) {
+  ChannelCtl* c = ch->ctl;
+  c->head.store(c->head.load(std::memory_order_relaxed) + 1, std::memory_order_release);
+  wake_all(&c->head);
+}
+
+// Receiver: waits for the next record and returns its slot index.
+int next_record(pace_kv_channel* ch, int timeout_ms, uint32_t* idx, const char* what) {
+  ChannelCtl* c = ch->ctl;
+  const uint32_t t = c->tail.load(std::memory_order_relaxed);
+  const uint64_t msg = ch->rx_msg;
+  const bool active = ch->rx_active;
+  PACE_KV_TRY(wait_for(ch, &c->head,
+                       [&] {
+                         return c->head.load(std::memory_order_acquire) != t ||
+                                (active && c->aborted_msg.load(std::memory_order_acquire) == msg);
+                       },
+                       timeout_ms, what));
+  if (c->head.load(std::memory_order_acquire) == t) {
+    ch->rx_active = false;
+    return fail(PACE_KV_ESTATE, "channel %s: the sender abandoned message %llu", ch->name.c_str(),
+                (unsigned long long)msg);
+  }
+  *idx = t % c->num_slots;
+  return PACE_KV_OK;
+}
+
+void release(pace_kv_channel* ch) {
+  ChannelCtl* c = ch->ctl;
+  c->tail.store(c->tail.load(std::memory_order_relaxed) + 1, std::memory_order_release);
+  wake_all(&c->tail);
+}
+
+int check_name(const char* name) {
+  if (name == nullptr || name[0] == '\0') return fail(PACE_KV_EINVAL, "channel: empty name");
+  if (strlen(name) > kNameMax) return fail(PACE_KV_EINVAL, "channel: name longer than %d bytes", kNameMax);
+  for (const char* p = name; *p; ++p)
+    if (*p == '/') return fail(PACE_KV_EINVAL, "channel: name must not contain '/'");
+  return PACE_KV_OK;
+}
+
+int map_channel(pace_kv_channel* ch, int64_t bytes) {
+  void* p = mmap(nullptr, static_cast<size_t>(bytes), PROT_READ | PROT_WRITE, MAP_SHARED, ch->fd, 0);
+  if (p == MAP_FAILED) return fail(PACE_KV_ESTATE, "channel %s: mmap failed: %s", ch->name.c_str(), strerror(errno));
+  ch->base = static_cast<char*>(p);
+  ch->map_bytes = bytes;
+  ch->ctl = reinterpret_cast<ChannelCtl*>(p);
+  return PACE_KV_OK;
+}
+
+void free_staging(Staging& s) {
+  for (int i = 0; i < 2; ++i) {
+    if (s.dev[i]) (void)hipFree(s.dev[i]);
+    if (s.pinned[i]) (void)hipHostFree(s.pinned[i]);
+    if (s.filled[i]) (void)hipEventDestroy(s.filled[i]);
+    if (s.copied[i]) (void)hipEventDestroy(s.copied[i]);
+    if (s.drained[i]) (void)hipEventDestroy(s.drained[i]);
+  }
+  if (s.copy) (void)hipStreamDestroy(s.copy);
+  s = Staging();
+}
+
+void destroy(pace_kv_channel* ch) {
+  free_staging(ch->tx);
+  free_staging(ch->rx);
+  delete ch->pool;
+  if (ch->base) munmap(ch->base, static_cast<size_t>(ch->map_bytes));
+  if (ch->fd >= 0) close(ch->fd);
+  if (ch->creator) shm_unlink(("/" + ch->name).c_str());
+  delete ch;
+}
+
+int new_endpoint(const char* name, int copy_threads, pace_kv_channel** out) {
+  if (out == nullptr) return fail(PACE_KV_EINVAL, "channel: out is NULL");
+  *out = nullptr;
+  PACE_KV_TRY(check_name(name));
+  if (copy_threads < 1 || copy_threads > 64) return fail(PACE_KV_EINVAL, "channel: copy_threads must be in [1, 64]");
+  pace_kv_channel* ch = new pace_kv_channel();
+  ch->name = name;
+  *out = ch;
+  return PACE_KV_OK;
+}
+
+// Device staging of one direction of an endpoint, created on its first
+// device transfer.
+int staging_ready(pace_kv_channel* ch, Staging& s) {
+  int dev = -1;
+  PACE_KV_TRY(hip_status(hipGetDevice(&dev), "hipGetDevice"));
+  if (s.ready) {
+    if (dev != s.device)
+      return fail(PACE_KV_ESTATE, "channel %s: staging lives on device %d, device %d is current",
+                  ch->name.c_str(), s.device, dev);
+    return PACE_KV_OK;
+  }
+  const size_t bytes = static_cast<size_t>(ch->ctl->slot_bytes);
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+    e = hipMalloc(reinterpret_cast<void**>(&s.dev[i]), bytes);
+    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&s.pinned[i]), bytes, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&s.filled[i], hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&s.copied[i], hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&s.drained[i], hipEventDisableTiming);
+  }
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&s.copy, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    free_staging(s);
+    return hip_status(e, "channel staging");
+  }
+  s.device = dev;
+  s.ready = true;
+  return PACE_KV_OK;
+}
+
+// Publishes the header record of a new message; returns its id.
+int send_header(pace_kv_channel* ch, int num_layers, int64_t n_pages, int64_t page_bytes, const void* meta,
+                int64_t meta_bytes, int timeout_ms, uint64_t* msg_id) {
+  ChannelCtl* c = ch->ctl;
+  if (meta_bytes < 0 || (meta_bytes > 0 && meta == nullptr))
+    return fail(PACE_KV_EINVAL, "channel: bad metadata");
+  if (meta_bytes > c->slot_bytes)
+    return fail(PACE_KV_ERANGE, "channel: metadata (%lld bytes) does not fit a slot (%lld bytes)",
+                (long long)meta_bytes, (long long)c->slot_bytes);
+  uint32_t idx = 0;
+  PACE_KV_TRY(acquire_slot(ch, timeout_ms, &idx));
+  const uint64_t id = c->next_msg_id.fetch_add(1) + 1;
+  if (meta_bytes > 0) memcpy(slot_data(ch, idx), meta, static_cast<size_t>(meta_bytes));
+  SlotRecord& r = c->slots[idx];
+  r.kind = kHeader;
+  r.chunk = 0;
+  r.msg_id = id;
+  r.offset = 0;
+  r.bytes = meta_bytes;
+  r.n_pages = n_pages;
+  r.page_bytes = page_bytes;
+  r.num_layers = num_layers;
+  publish(ch);
+  if (msg_id) *msg_id = id;
+  return PACE_KV_OK;
+}
+
+int send_chunk_from(pace_kv_channel* ch, uint64_t id, int64_t c, const Chunking::Chunk& k, const char* src,
+                    int timeout_ms) {
+  uint32_t idx = 0;
+  PACE_KV_TRY(acquire_slot(ch, timeout_ms, &idx));
+  ch->pool->copy(slot_data(ch, idx), src, k.bytes);
+  SlotRecord& r = ch->ctl->slots[idx];
+  r.kind = kData;
+  r.chunk = static_cast<uint32_t>(c);
+  r.msg_id = id;
+  r.offset = k.offset;
+  r.bytes = k.bytes;
+  publish(ch);
+  return PACE_KV_OK;
+}
+
+// Marks a message whose chunks will not all arrive, so that the receiver
+// fails at once instead of waiting out its deadline.
+int abandon(pace_kv_channel* ch, uint64_t id, int rc) {
+  ch->ctl->aborted_msg.store(id, std::memory_order_release);
+  wake_all(&ch->ctl->head);
+  return rc;
+}
+
+int check_rx_shape(pace_kv_channel* ch, int num_layers, int64_t n_pages, int64_t page_bytes) {
+  if (!ch->rx_active)
+    return fail(PACE_KV_ESTATE, "channel %s: no message header received", ch->name.c_str());
+  const Chunking& k = ch->rx_chunks;
+  if (num_layers != k.num_layers || n_pages != k.n_pages || page_bytes != k.page_bytes)
+    return fail(PACE_KV_EINVAL,
+                "channel %s: message %llu holds %d layers x %lld pages x %lld bytes, the receiver "
+                "asked for %d x %lld x %lld", ch->name.c_str(), (unsigned long long)ch->rx_msg,
+                k.num_layers, (long long)k.n_pages, (long long)k.page_bytes, num_layers,
+                (long long)n_pages, (long long)page_bytes);
+  return PACE_KV_OK;
+}
+
+// Receiver: waits for chunk rx_next of the current message and checks it.
+int next_chunk(pace_kv_channel* ch, int timeout_ms, uint32_t* idx, Chunking::Chunk* k) {
+  PACE_KV_TRY(next_record(ch, timeout_ms, idx, "a payload chunk"));
+  const SlotRecord& r = ch->ctl->slots[*idx];
+  *k = ch->rx_chunks.at(ch->rx_next);
+  if (r.kind != kData || r.msg_id != ch->rx_msg || r.chunk != static_cast<uint32_t>(ch->rx_next) ||
+      r.offset != k->offset || r.bytes != k->bytes) {
+    ch->rx_active = false;
+    return fail(PACE_KV_ESTATE, "channel %s: expected chunk %lld of message %llu, found a record of "
+                "kind %u for message %llu chunk %u", ch->name.c_str(), (long long)ch->rx_next,
+                (unsigned long long)ch->rx_msg, r.kind, (unsigned long long)r.msg_id, r.chunk);
+  }
+  return PACE_KV_OK;
+}
+
+void finish_chunk(pace_kv_channel* ch) {
+  release(ch);
+  if (++ch->rx_next == ch->rx_chunks.num_chunks) ch->rx_active = false;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pace_kv_channel_create(const char* name, int64_t slot_bytes, int num_slots, int copy_threads,
+                           pace_kv_channel** out) {
+  PACE_KV_TRY(new_endpoint(name, copy_threads, out));
+  pace_kv_channel* ch = *out;
+  *out = nullptr;
+  if (slot_bytes <= 0 || slot_bytes % 4096 != 0) {
+    delete ch;
+    return fail(PACE_KV_EINVAL, "channel: slot_bytes must be a positive multiple of 4096");
+  }
+  if (num_slots < 2 || num_slots > kMaxSlots) {
+    delete ch;
+    return fail(PACE_KV_EINVAL, "channel: num_slots must be in [2, %d]", kMaxSlots);
+  }
+  if (slot_bytes > (INT64_MAX / 2) / num_slots) {
+    delete ch;
+    return fail(PACE_KV_ERANGE, "channel: ring size overflows");
+  }
+  const int64_t data_offset = round_up(static_cast<int64_t>(sizeof(ChannelCtl)), 1 << 21);
+  const int64_t total = data_offset + slot_bytes * num_slots;
+  ch->fd = shm_open(("/" + ch->name).c_str(), O_CREAT | O_EXCL | O_RDWR, 0600);
+  if (ch->fd < 0) {
+    const int err = errno;
+    delete ch;
+    return fail(err == EEXIST ? PACE_KV_ESTATE : PACE_KV_EINVAL, "channel %s: shm_open failed: %s", name,
+                strerror(err));
+  }
+  ch->creator = true;
+  ch->pool = new CopyPool(copy_threads);
+  if (ftruncate(ch->fd, total) != 0) {
+    const int err = errno;
+    destroy(ch);
+    return fail(PACE_KV_ENOMEM, "channel %s: cannot size the ring to %lld bytes: %s", name, (long long)total,
+                strerror(err));
+  }
+  int rc = map_channel(ch, total);
+  if (rc) {
+    destroy(ch);
+    return rc;
+  }
+  ChannelCtl* c = ch->ctl;
+  c->version = kVersion;
+  c->num_slots = static_cast<uint32_t>(num_slots);
+  c->slot_bytes = slot_bytes;
+  c->data_offset = data_offset;
+  c->total_bytes = total;
+  c->head.store(0);
+  c->tail.store(0);
+  c->closed.store(0);
+  c->next_msg_id.store(0);
+  c->aborted_msg.store(0);
+  std::atomic_thread_fence(std::memory_order_release);
+  // The magic goes in last: an opener that sees it sees a complete block.
+  __atomic_store_n(&c->magic, kMagic, __ATOMIC_RELEASE);
+  *out = ch;
+  return PACE_KV_OK;
+}
+
+int pace_kv_channel_open(const char* name, int copy_threads, int timeout_ms, pace_kv_channel** out) {
+  PACE_KV_TRY(new_endpoint(name, copy_threads, out));
+  pace_kv_channel* ch = *out;
+  *out = nullptr;
+  using clock = std::chrono::steady_clock;
+  const auto deadline = clock::now() + std::chrono::milliseconds(timeout_ms < 0 ? 0 : timeout_ms);
+  // Waits for the creator: the name, then its size, then the magic.
+  struct stat st;
+  for (;;) {
+    if (ch->fd < 0) ch->fd = shm_open(("/" + ch->name).c_str(), O_RDWR, 0600);
+    if (ch->fd >= 0 && fstat(ch->fd, &st) == 0 && st.st_size >= static_cast<off_t>(sizeof(ChannelCtl))) {
+      if (!ch->base) {
+        int rc = map_channel(ch, st.st_size);
+        if (rc) {
+          destroy(ch);
+          return rc;
+        }
+      }
+      if (__atomic_load_n(&ch->ctl->magic, __ATOMIC_ACQUIRE) == kMagic) break;
+    }
+    if (clock::now() >= deadline) {
+      destroy(ch);
+      return fail(PACE_KV_ETIMEDOUT, "channel %s: not created within %d ms", name, timeout_ms);
+    }
+    std::this_thread::sleep_for(std::chrono::milliseconds(1));
+  }
+  ChannelCtl* c = ch->ctl;
+  if (c->version != kVersion || c->total_bytes != ch->map_bytes || c->num_slots < 2 ||
+      c->num_slots > kMaxSlots) {
+    destroy(ch);
+    return fail(PACE_KV_ESTATE, "channel %s: incompatible control block", name);
+  }
+  ch->pool = new CopyPool(copy_threads);
+  *out = ch;
+  return PACE_KV_OK;
+}
+
+int pace_kv_channel_close(pace_kv_channel* ch) {
+  if (ch == nullptr) return PACE_KV_OK;
+  if (ch->ctl) {
+    ch->ctl->closed.store(1, std::memory_order_release);
+    wake_all(&ch->ctl->head);
+    wake_all(&ch->ctl->tail);
+  }
+  // Copies and kernels this endpoint enqueued may still use its staging.
+  for (Staging* s : {&ch->tx, &ch->rx}) {
+    if (!s->ready) continue;
+    (void)hipStreamSynchronize(s->copy);
+    for (int i = 0; i < 2; ++i) (void)hipEventSynchronize(s->drained[i]);
+  }
+  destroy(ch);
+  return PACE_KV_OK;
+}
+
+int pace_kv_channel_info(pace_kv_channel* ch, int64_t* slot_bytes, int* num_slots) {
+  if (ch == nullptr) return fail(PACE_KV_EINVAL, "channel is NULL");
+  if (slot_bytes) *slot_bytes = ch->ctl->slot_bytes;
+  if (num_slots) *num_slots = static_cast<int>(ch->ctl->num_slots);
+  return PACE_KV_OK;
+}
+
+int pace_kv_channel_send(pace_kv_channel* ch, const void* const* src_layers, int num_layers,
+                         int64_t pool_pages, const int32_t* page_ids, int64_t n_pages, int64_t page_bytes,
+                         const void* meta, int64_t meta_bytes, int timeout_ms, uint64_t* msg_id,
+                         void* stream_) {
+  if (ch == nullptr) return fail(PACE_KV_EINVAL, "channel is NULL");
+  std::lock_guard<std::mutex> lock(ch->send_mu);
+  Chunking k;
+  PACE_KV_TRY(make_chunking(num_layers, n_pages, page_bytes, ch->ctl->slot_bytes, &k));
+  if (k.num_chunks > 0) {
+    if (src_layers == nullptr || page_ids == nullptr) return fail(PACE_KV_EINVAL, "channel send: NULL argument");
+    PACE_KV_TRY(staging_ready(ch, ch->tx));
+  }
+  uint64_t id = 0;
+  PACE_KV_TRY(send_header(ch, num_layers, n_pages, page_bytes, meta, meta_bytes, timeout_ms, &id));
+  if (msg_id) *msg_id = id;
+  Staging& s = ch->tx;
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  // Chunk c: pack into device slot c%2 (caller stream), copy down to pinned
+  // slot c%2 (copy stream); chunk c-1 is copied into the ring meanwhile.
+  for (int64_t c = 0; c <= k.num_chunks; ++c) {
+    if (c < k.num_chunks) {
+      const int b = static_cast<int>(c & 1);
+      const Chunking::Chunk ck = k.at(c);
+      int rc = hip_status(hipStreamWaitEvent(stream, s.copied[b], 0), "channel send wait");
+      if (rc == PACE_KV_OK) {
+        const int64_t stride = k.layers_per_chunk > 0 ? k.layer_bytes : ck.bytes;
+        rc = pace_kv_pack(src_layers + ck.layer, ck.nl, pool_pages, page_ids + ck.j0, ck.nj, page_bytes,
+                          s.dev[b], stride, nullptr, stream);
+      }
+      if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(s.filled[b], stream), "channel send record");
+      if (rc == PACE_KV_OK) rc = hip_status(hipStreamWaitEvent(s.copy, s.filled[b], 0), "channel send wait");
+      if (rc == PACE_KV_OK)
+        rc = hip_status(hipMemcpyAsync(s.pinned[b], s.dev[b], static_cast<size_t>(ck.bytes),
+                                       hipMemcpyDeviceToHost, s.copy), "channel device-to-host copy");
+      if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(s.copied[b], s.copy), "channel send record");
+      if (rc) return abandon(ch, id, rc);
+    }
+    if (c > 0) {
+      const int b = static_cast<int>((c - 1) & 1);
+      int rc = hip_status(hipEventSynchronize(s.copied[b]), "channel device-to-host copy");
+      if (rc == PACE_KV_OK) rc = send_chunk_from(ch, id, c - 1, k.at(c - 1), s.pinned[b], timeout_ms);
+      if (rc) return abandon(ch, id, rc);
+    }
+  }
+  return PACE_KV_OK;
+}
+
+int pace_kv_channel_send_host(pace_kv_channel* ch, const void* payload, int num_layers, int64_t n_pages,
+                              int64_t page_bytes, const void* meta, int64_t meta_bytes, int timeout_ms,
+                              uint64_t* msg_id) {
+  if (ch == nullptr) return fail(PACE_KV_EINVAL, "channel is NULL");
+  std::lock_guard<std::mutex> lock(ch->send_mu);
+  Chunking k;
+  PACE_KV_TRY(make_chunking(num_layers, n_pages, page_bytes, ch->ctl->slot_bytes, &k));
+  if (k.num_chunks > 0 && payload == nullptr) return fail(PACE_KV_EINVAL, "channel send: payload is NULL");
+  uint64_t id = 0;
+  PACE_KV_TRY(send_header(ch, num_layers, n_pages, page_bytes, meta, meta_bytes, timeout_ms, &id));
+  if (msg_id) *msg_id = id;
+  for (int64_t c = 0; c < k.num_chunks; ++c) {
+    const Chunking::Chunk ck = k.at(c);
+    int rc = send_chunk_from(ch, id, c, ck, static_cast<const char*>(payload) + ck.offset, timeout_ms);
+    if (rc) return abandon(ch, id, rc);
+  }
+  return PACE_KV_OK;
+}
+
+int pace_kv_channel_recv_header(pace_kv_channel* ch, void* meta, int64_t meta_cap, int64_t* meta_bytes,
+                                int* num_layers, int64_t* n_pages, int64_t* page_bytes, uint64_t* msg_id,
+                                int timeout_ms) {
+  if (ch == nullptr) return fail(PACE_KV_EINVAL, "channel is NULL");
+  std::lock_guard<std::mutex> lock(ch->recv_mu);
+  if (ch->rx_active)
+    return fail(PACE_KV_ESTATE, "channel %s: the payload of message %llu has not been received",
+                ch->name.c_str(), (unsigned long long)ch->rx_msg);
+  uint32_t idx = 0;
+  for (;;) {
+    PACE_KV_TRY(next_record(ch, timeout_ms, &idx, "a message"));
+    if (ch->ctl->slots[idx].kind == kHeader) break;
+    // A chunk without its header: the rest of a message whose receive
+    // failed part-way.  It is dropped.
+    release(ch);
+  }
+  const SlotRecord& r = ch->ctl->slots[idx];
+  if (meta_bytes) *meta_bytes = r.bytes;
+  if (r.bytes > meta_cap || (r.bytes > 0 && meta == nullptr))
+    return fail(PACE_KV_ERANGE, "channel %s: metadata needs %lld bytes, the buffer holds %lld (message kept)",
+                ch->name.c_str(), (long long)r.bytes, (long long)meta_cap);
+  Chunking k;
+  int rc = make_chunking(r.num_layers, r.n_pages, r.page_bytes, ch->ctl->slot_bytes, &k);
+  if (rc) {
+    release(ch);
+    return rc;
+  }
+  if (r.bytes > 0) memcpy(meta, slot_data(ch, idx), static_cast<size_t>(r.bytes));
+  if (num_layers) *num_layers = r.num_layers;
+  if (n_pages) *n_pages = r.n_pages;
+  if (page_bytes) *page_bytes = r.page_bytes;
+  if (msg_id) *msg_id = r.msg_id;
+  ch->rx_msg = r.msg_id;
+  ch->rx_chunks = k;
+  ch->rx_next = 0;
+  ch->rx_active = k.num_chunks > 0;
+  release(ch);
+  return PACE_KV_OK;
+}
+
+int pace_kv_channel_recv(pace_kv_channel* ch, void* const* dst_layers, int num_layers, int64_t pool_pages,
+                         const int32_t* page_ids, int64_t n_pages, int64_t page_bytes, int32_t* err_count,
+                         int timeout_ms, void* stream_) {
+  if (ch == nullptr) return fail(PACE_KV_EINVAL, "channel is NULL");
+  std::lock_guard<std::mutex> lock(ch->recv_mu);
+  PACE_KV_TRY(check_rx_shape(ch, num_layers, n_pages, page_bytes));
+  if (dst_layers == nullptr || page_ids == nullptr) return fail(PACE_KV_EINVAL, "channel recv: NULL argument");
+  PACE_KV_TRY(staging_ready(ch, ch->rx));
+  const Chunking k = ch->rx_chunks;
+  Staging& s = ch->rx;
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  // The caller's earlier work on `stream` (e.g. the upload of page_ids, or
+  // earlier use of the destination pages) comes before the unpacks, which
+  // run on `stream` itself.
+  while (ch->rx_active) {
+    const int64_t c = ch->rx_next;
+    const int b = static_cast<int>(c & 1);
+    uint32_t idx = 0;
+    Chunking::Chunk ck;
+    PACE_KV_TRY(next_chunk(ch, timeout_ms, &idx, &ck));
+    // pinned slot b was last read by the upload of chunk c-2
+    int rc = hip_status(hipEventSynchronize(s.copied[b]), "channel host-to-device copy");
+    if (rc) {
+      ch->rx_active = false;
+      return rc;
+    }
+    ch->pool->copy(s.pinned[b], slot_data(ch, idx), ck.bytes);
+    finish_chunk(ch);
+    // device slot b was last read by the unpack of chunk c-2
+    rc = hip_status(hipStreamWaitEvent(s.copy, s.drained[b], 0), "channel recv wait");
+    if (rc == PACE_KV_OK)
+      rc = hip_status(hipMemcpyAsync(s.dev[b], s.pinned[b], static_cast<size_t>(ck.bytes), hipMemcpyHostToDevice,
+                                     s.copy), "channel host-to-device copy");
+    if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(s.copied[b], s.copy), "channel recv record");
+    if (rc == PACE_KV_OK) rc = hip_status(hipStreamWaitEvent(stream, s.copied[b], 0), "channel recv wait");
+    if (rc == PACE_KV_OK) {
+      const int64_t stride = k.layers_per_chunk > 0 ? k.layer_bytes : ck.bytes;
+      rc = pace_kv_unpack(s.dev[b], stride, dst_layers + ck.layer, ck.nl, pool_pages, page_ids + ck.j0, ck.nj,
+                          page_bytes, err_count, stream);
+    }
+    if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(s.drained[b], stream), "channel recv record");
+    if (rc) {
+      ch->rx_active = false;
+      return rc;
+    }
+  }
+  return PACE_KV_OK;
+}
+
+int pace_kv_channel_recv_host(pace_kv_channel* ch, void* payload, int64_t payload_bytes, int timeout_ms) {
+  if (ch == nullptr) return fail(PACE_KV_EINVAL, "channel is NULL");
+  std::lock_guard<std::mutex> lock(ch->recv_mu);
+  if (!ch->rx_active) return fail(PACE_KV_ESTATE, "channel %s: no message header received", ch->name.c_str());
+  const Chunking& k = ch->rx_chunks;
+  const int64_t total = k.num_layers * k.layer_bytes;
+  if (payload != nullptr && payload_bytes != total)
+    return fail(PACE_KV_EINVAL, "channel %s: message %llu holds %lld payload bytes, the buffer %lld",
+                ch->name.c_str(), (unsigned long long)ch->rx_msg, (long long)total, (long long)payload_bytes);
+  while (ch->rx_active) {
+    uint32_t idx = 0;
+    Chunking::Chunk ck;
+    PACE_KV_TRY(next_chunk(ch, timeout_ms, &idx, &ck));
+    if (payload != nullptr) ch->pool->copy(static_cast<char*>(payload) + ck.offset, slot_data(ch, idx), ck.bytes);
+    finish_chunk(ch);
+  }
+  return PACE_KV_OK;
+}
+
+}  // extern "C"

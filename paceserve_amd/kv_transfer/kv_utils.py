@@ -182,6 +182,75 @@ class KVhelper:
 
     # ------------------------------------------------------ additive API
 
+    def send_kv_cache(self, seq, seq_manager, channel, left_prefill=None, kv_transfer_start=None,
+                      timeout: float = 60.0):
+        """get_kv_cache through a KVChannel: packs the sequence's pages out of
+        this cache into the channel (the zero-page fallback travels as one
+        zero page, as get_kv_cache returns it) and returns the KVref that
+        replaces the KVobj on the control plane.  Raises like get_kv_cache,
+        plus PaceKVError from the channel."""
+        from .channel import KVref, kv_size_mb
+
+        try:
+            kv_page_indices = seq_manager._get_block_table(seq)
+        except Exception:
+            print(f"seq {seq.seq_id} was not allocated any memory")
+            kv_page_indices = None
+        shape = self.page_shape()
+        if not kv_page_indices:
+            zeros = torch.zeros(self.num_layers, 1, *shape, dtype=self.dtype)
+            ref = KVref(seq.seq_id, [0], kv_size_mb(self.num_layers, 1, zeros[0, 0].numel() * zeros.element_size()),
+                        left_prefill, kv_transfer_start)
+            ref.msg_id = channel.send_host(zeros, ref.meta(), timeout)
+            return ref
+        pool = self.pool()
+        ids = normalize_page_ids(kv_page_indices, pool.num_pages)
+        ref = KVref(seq.seq_id, list(kv_page_indices), kv_size_mb(self.num_layers, len(ids), pool.page_bytes),
+                    left_prefill, kv_transfer_start)
+        with torch.cuda.device(pool.device):
+            ref.msg_id = channel.send(pool, ids, ref.meta(), timeout)
+        return ref
+
+    def recv_kv_cache(self, channel, kv_indices, device, timeout: float = 60.0) -> bool:
+        """insert_kv_cache of the channel message whose header was just
+        received: writes its pages to kv_indices of this cache.  Returns
+        False on any error (printed, as insert_kv_cache does), after draining
+        the message so that the channel stays usable."""
+        try:
+            self._recv(channel, kv_indices, device, timeout)
+            return True
+        except Exception as e:
+            print(f"error during insert kv cache: {e}")
+            try:
+                channel.discard(timeout)
+            except Exception:
+                pass
+            return False
+
+    def _recv(self, channel, kv_indices, device, timeout: float) -> None:
+        h = channel._current()
+        dev = torch.device(device) if not isinstance(device, int) else torch.device("cuda", device)
+        if dev.type != "cuda":
+            raise RuntimeError(f"cannot insert into a device cache from device {dev}")
+        pool = self.pool()
+        ids_in = list(kv_indices)
+        ids = normalize_page_ids(ids_in, pool.num_pages) if ids_in else []
+        if h.num_layers < self.num_layers or h.page_bytes != pool.page_bytes:
+            raise RuntimeError(f"message {h.msg_id} holds {h.num_layers} layers of {h.page_bytes}-byte pages; "
+                               f"the cache has {self.num_layers} layers of {pool.page_bytes}-byte pages")
+        if h.num_layers == self.num_layers and ids and len(ids) == h.n_pages and len(set(ids)) == len(ids):
+            with torch.cuda.device(pool.device):
+                channel.recv(pool, ids, timeout)
+                torch.cuda.current_stream(pool.device).synchronize()
+            return
+        # Repeated ids (the last write wins), a one-page broadcast, surplus
+        # layers or an empty id list: take the payload to host memory and
+        # insert it with insert_kv_cache's rules.
+        host = torch.empty((h.num_layers, h.n_pages) + pool.page_shape, dtype=pool.dtype, pin_memory=True)
+        channel.recv_host(host, timeout)
+        with self._lock:                 # the insert uses the shared stager
+            self._insert(host, ids_in, device)
+
     def pack_pages(self, page_ids, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Device-resident pack of this cache's pages: [L, n, 2, P, H, D]."""
         pool = self.pool()

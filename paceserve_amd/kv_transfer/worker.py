@@ -8,6 +8,9 @@ Mirrors the three RPC methods of BaseWorker that reach KVhelper
                                  :245-247);
   - _insert_kv_cache(seq, kv_obj, device) -> KVStatus, or False when the
     destination cannot hold the sequence (:249-281).
+and, over a cross-process KVChannel in place of a KVobj returned through
+Ray, _send_kv_cache / _recv_kv_cache with the same free, allocation and
+remap rules.
 
 Two reference defects are not reproduced: the allocate time is reported as
 a positive duration (the reference subtracts the later stamp from the earlier
@@ -84,6 +87,46 @@ class KVWorkerMixin:
         # generated token opened a page) leaves that last page untouched.
         ids = kv_indices if len(kv_indices) == block_len else kv_indices[:-1]
         status = self.kvhelper.insert_kv_cache(cached_content, ids, device)
+        insert_time = time.monotonic() - insert_start
+        return KVStatus(status, insert_time, insert_start - allocate_start)
+
+
+    # ------------------------------------------------ cross-process channel
+
+    def _send_kv_cache(self, seq, channel, left_prefill=None, kv_transfer_start=None):
+        """_get_kv_cache through a KVChannel: the pages go into the channel,
+        the sequence's source pages are freed, and (KVref, local_rank) is
+        returned for the control plane in place of the KVobj's tensor."""
+        ref = self.kvhelper.send_kv_cache(seq, self.seq_manager, channel, left_prefill, kv_transfer_start)
+        self.seq_manager._free_seq(seq.seq_id)
+        return (ref, self.local_rank)
+
+    def _recv_kv_cache(self, seq, channel, device, timeout: float = 60.0):
+        """_insert_kv_cache of the next channel message, which must carry
+        `seq`: allocates the destination pages, receives the pages into them
+        and returns KVStatus; False (with the message drained) when the
+        destination cannot hold the sequence or the message is another
+        sequence's."""
+        from .channel import KVref
+
+        h = channel.recv_header(timeout)
+        ref = KVref.from_header(h)
+        if ref.seq_id != seq.seq_id:
+            channel.discard(timeout)
+            return False
+        block_len = len(ref.kv_indices)
+        allocate_start = time.monotonic()
+        bm = self.seq_manager.block_manager
+        if bm.get_num_free_gpu_blocks() >= bm.get_num_initial_blocks(seq):
+            self.seq_manager.add_seq(seq)
+            bm.allocate(seq)
+        else:
+            channel.discard(timeout)
+            return False
+        kv_indices = self.seq_manager._get_block_table(seq)
+        insert_start = time.monotonic()
+        ids = kv_indices if len(kv_indices) == block_len else kv_indices[:-1]
+        status = self.kvhelper.recv_kv_cache(channel, ids, device, timeout)
         insert_time = time.monotonic() - insert_start
         return KVStatus(status, insert_time, insert_start - allocate_start)
 

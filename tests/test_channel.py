@@ -1,0 +1,270 @@
+"""The cross-process channel's protocol on host payloads (no GPU): messages in
+order with their metadata, payloads larger than the ring streaming through
+it, layer- and page-sized chunks, another process as the sender, deadlines,
+closing, abandoned messages, draining, and argument errors."""
+import os
+import subprocess
+import sys
+import threading
+import time
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from paceserve_amd import _native
+from paceserve_amd.kv_transfer.channel import KVChannel, KVref, MessageHeader
+
+ROOT = Path(__file__).resolve().parent.parent
+_count = [0]
+
+
+def name():
+    _count[0] += 1
+    return f"pace_test_{os.getpid()}_{_count[0]}"
+
+
+def status(excinfo):
+    return excinfo.value.status
+
+
+def payload(L, n, page_shape, seed, dtype=torch.float16):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn((L, n) + tuple(page_shape), generator=g).to(dtype)
+
+
+def pair(slot_bytes=64 << 10, num_slots=3, threads=4):
+    nm = name()
+    rx = KVChannel.create(nm, slot_bytes, num_slots, threads)
+    tx = KVChannel.open(nm, threads, timeout=5)
+    return tx, rx
+
+
+# (L, n, page_shape): page chunks (a layer is larger than a 64 KiB slot),
+# layer chunks, a single page, more layers than one launch takes
+SHAPES = [(3, 40, (2, 16, 1, 64)), (8, 5, (2, 4, 2, 16)), (1, 1, (2, 1, 1, 8)), (70, 3, (2, 2, 1, 8))]
+
+
+def test_messages_arrive_in_order_with_their_metadata():
+    tx, rx = pair()
+    sent = [(payload(L, n, ps, i), f"msg {i}".encode()) for i, (L, n, ps) in enumerate(SHAPES)]
+    ids = []
+
+    def send():
+        for p, m in sent:
+            ids.append(tx.send_host(p, m, timeout=10))
+
+    t = threading.Thread(target=send)
+    t.start()
+    got = []
+    for p, m in sent:
+        h = rx.recv_header(timeout=10)
+        assert h.meta == m and (h.num_layers, h.n_pages) == tuple(p.shape[:2])
+        assert h.page_bytes == p[0, 0].numel() * 2
+        out = torch.empty_like(p)
+        rx.recv_host(out, timeout=10)
+        got.append((h.msg_id, out))
+    t.join()
+    assert [g[0] for g in got] == ids == sorted(ids)
+    for (p, _), (_, out) in zip(sent, got):
+        assert torch.equal(p.view(torch.int16), out.view(torch.int16))
+    tx.close()
+    rx.close()
+
+
+def test_payload_larger_than_the_ring_streams_through_it():
+    tx, rx = pair(slot_bytes=4096, num_slots=2)
+    p = payload(4, 300, (2, 4, 1, 16), 7)          # 300 pages of 256 B per layer: 19 page chunks per layer
+    assert p.numel() * 2 > 20 * rx.slot_bytes * rx.num_slots
+    t = threading.Thread(target=lambda: tx.send_host(p, b"big", timeout=10))
+    t.start()
+    h = rx.recv_header(timeout=10)
+    out = torch.empty_like(p)
+    rx.recv_host(out, timeout=10)
+    t.join()
+    assert h.meta == b"big" and torch.equal(out.view(torch.int16), p.view(torch.int16))
+    tx.close()
+    rx.close()
+
+
+SENDER = r"""
+import sys, torch
+sys.path.insert(0, {root!r})
+from paceserve_amd.kv_transfer.channel import KVChannel
+ch = KVChannel.open({name!r}, 4, timeout=30)
+for i in range(5):
+    g = torch.Generator().manual_seed(100 + i)
+    p = torch.randint(0, 256, (6, 7 + i, 2, 4, 1, 16), generator=g, dtype=torch.uint8)
+    ch.send_host(p, ("from child %d" % i).encode(), timeout=30)
+ch.close()
+"""
+
+
+def test_another_process_sends():
+    nm = name()
+    rx = KVChannel.create(nm, 8192, 3, 4)
+    child = subprocess.Popen([sys.executable, "-c", SENDER.format(root=str(ROOT), name=nm)])
+    try:
+        for i in range(5):
+            h = rx.recv_header(timeout=60)
+            assert h.meta == f"from child {i}".encode()
+            out = torch.empty((6, 7 + i, 2, 4, 1, 16), dtype=torch.uint8)
+            rx.recv_host(out, timeout=60)
+            g = torch.Generator().manual_seed(100 + i)
+            assert torch.equal(out, torch.randint(0, 256, out.shape, generator=g, dtype=torch.uint8))
+        assert child.wait(timeout=60) == 0
+    finally:
+        if child.poll() is None:
+            child.kill()
+        rx.close()
+
+
+def test_waits_end_at_their_deadline():
+    tx, rx = pair()
+    t0 = time.monotonic()
+    with pytest.raises(_native.PaceKVError) as e:
+        rx.recv_header(timeout=0.2)
+    assert status(e) == _native.PACE_KV_ETIMEDOUT
+    assert 0.15 < time.monotonic() - t0 < 5
+    # a full ring: the sender's wait for a free slot ends too
+    with pytest.raises(_native.PaceKVError) as e:
+        tx.send_host(payload(4, 40, (2, 16, 1, 64), 1), timeout=0.2)
+    assert status(e) == _native.PACE_KV_ETIMEDOUT
+    tx.close()
+    rx.close()
+
+
+def test_closing_wakes_the_peer():
+    tx, rx = pair()
+    seen = []
+
+    def wait():
+        try:
+            rx.recv_header(timeout=30)
+        except _native.PaceKVError as exc:
+            seen.append(exc.status)
+
+    t = threading.Thread(target=wait)
+    t.start()
+    time.sleep(0.2)
+    tx.close()
+    t.join(timeout=10)
+    assert seen == [_native.PACE_KV_ECLOSED]
+    rx.close()
+
+
+def test_abandoned_message_fails_the_receiver_and_the_channel_recovers():
+    tx, rx = pair(slot_bytes=4096, num_slots=2)
+    big = payload(2, 64, (2, 4, 1, 16), 3)         # 16 chunks through 2 slots
+    h = None
+    errs = []
+
+    def send():
+        try:
+            tx.send_host(big, b"big", timeout=0.3)
+        except _native.PaceKVError as exc:
+            errs.append(exc.status)
+
+    t = threading.Thread(target=send)
+    t.start()
+    h = rx.recv_header(timeout=10)
+    assert h.meta == b"big"
+    t.join(timeout=10)                               # the receiver took nothing: the sender gave up
+    assert errs == [_native.PACE_KV_ETIMEDOUT]
+    with pytest.raises(_native.PaceKVError) as e:
+        rx.recv_host(torch.empty_like(big), timeout=5)
+    assert status(e) == _native.PACE_KV_ESTATE and "abandoned" in str(e.value)
+    # the chunks already in the ring are skipped; the next message arrives whole
+    small = payload(1, 2, (2, 4, 1, 16), 4)
+    t = threading.Thread(target=lambda: tx.send_host(small, b"next", timeout=10))
+    t.start()
+    h = rx.recv_header(timeout=10)
+    out = torch.empty_like(small)
+    rx.recv_host(out, timeout=10)
+    t.join()
+    assert h.meta == b"next" and torch.equal(out.view(torch.int16), small.view(torch.int16))
+    tx.close()
+    rx.close()
+
+
+def test_discarded_payload_leaves_the_next_message_intact():
+    tx, rx = pair(slot_bytes=4096, num_slots=2)
+    a, b = payload(3, 30, (2, 4, 1, 16), 5), payload(2, 3, (2, 4, 1, 16), 6)
+
+    def send():
+        tx.send_host(a, b"a", timeout=10)
+        tx.send_host(b, b"b", timeout=10)
+
+    t = threading.Thread(target=send)
+    t.start()
+    assert rx.recv_header(timeout=10).meta == b"a"
+    rx.discard(timeout=10)
+    assert rx.recv_header(timeout=10).meta == b"b"
+    out = torch.empty_like(b)
+    rx.recv_host(out, timeout=10)
+    t.join()
+    assert torch.equal(out.view(torch.int16), b.view(torch.int16))
+    tx.close()
+    rx.close()
+
+
+def test_large_metadata_and_empty_payload():
+    tx, rx = pair(slot_bytes=256 << 10)
+    ref = KVref("seq-9", list(range(20000)), 1.5, 3.0, 4.0)
+    meta = ref.meta()
+    assert len(meta) > 64 << 10                      # more than recv_header's first buffer
+    tx.send_host(torch.empty((0, 0, 2, 4, 1, 16), dtype=torch.float16), meta, timeout=5)
+    h = rx.recv_header(timeout=5)
+    assert h.payload_bytes == 0
+    back = KVref.from_header(h)
+    assert (back.seq_id, back.kv_indices, back.size, back.msg_id) == ("seq-9", ref.kv_indices, 1.5, h.msg_id)
+    with pytest.raises(RuntimeError):
+        rx.recv_host(torch.empty(1))               # nothing pending
+    tx.close()
+    rx.close()
+
+
+def test_argument_errors():
+    lib = _native.load()
+    h = __import__("ctypes").c_void_p()
+    for bad_name in (b"", b"a/b", b"x" * 300):
+        assert lib.pace_kv_channel_create(bad_name, 4096, 2, 1, __import__("ctypes").byref(h)) == _native.PACE_KV_EINVAL
+    nm = name()
+    for slot, slots, thr in ((100, 2, 1), (4096, 1, 1), (4096, 65, 1), (4096, 2, 0)):
+        with pytest.raises(_native.PaceKVError) as e:
+            KVChannel.create(nm, slot, slots, thr)
+        assert status(e) == _native.PACE_KV_EINVAL
+    rx = KVChannel.create(nm, 4096, 2, 1)
+    with pytest.raises(_native.PaceKVError) as e:
+        KVChannel.create(nm, 4096, 2, 1)
+    assert status(e) == _native.PACE_KV_ESTATE
+    with pytest.raises(_native.PaceKVError) as e:
+        KVChannel.open(name() + "_missing", 1, timeout=0)
+    assert status(e) == _native.PACE_KV_ETIMEDOUT
+    tx = KVChannel.open(nm, 1, timeout=5)
+    with pytest.raises(_native.PaceKVError) as e:
+        tx.send_host(payload(1, 1, (2, 4, 1, 16), 0), b"m" * 5000, timeout=1)   # metadata > slot
+    assert status(e) == _native.PACE_KV_ERANGE
+    with pytest.raises(_native.PaceKVError) as e:
+        tx.send_host(payload(1, 1, (2, 64, 1, 64), 0), timeout=1)               # page > slot
+    assert status(e) == _native.PACE_KV_ERANGE
+    assert lib.pace_kv_channel_recv_host(rx._handle, None, 0, 0) == _native.PACE_KV_ESTATE   # no header
+    tx.send_host(payload(2, 2, (2, 4, 1, 16), 0), timeout=1)
+    rx.recv_header(timeout=1)
+    assert lib.pace_kv_channel_recv_header(rx._handle, None, 0, None, None, None, None, None, 0) == \
+        _native.PACE_KV_ESTATE                                                   # payload pending
+    out = torch.empty((2, 3, 2, 4, 1, 16), dtype=torch.float16)
+    assert lib.pace_kv_channel_recv_host(rx._handle, out.data_ptr(), out.numel() * 2, 0) == _native.PACE_KV_EINVAL
+    rx.discard(timeout=1)
+    tx.close()
+    rx.close()
+    assert not os.path.exists(f"/dev/shm/{nm}")                                  # the creator unlinked it
+
+
+def test_kvref_round_trips_the_kvobj_fields():
+    r = KVref(17, [5, 3, 9], 2.25, 1.0, 2.0, 0)
+    h = MessageHeader(42, r.meta(), 32, 3, 65536)
+    b = KVref.from_header(h)
+    assert (b.seq_id, b.kv_indices, b.size, b.left_prefill, b.kv_transfer_start, b.msg_id) == \
+        (17, [5, 3, 9], 2.25, 1.0, 2.0, 42)

@@ -1,0 +1,311 @@
+"""The cross-process channel on the GPU: pages packed out of one pool and
+unpacked into another through the shared-memory ring, checked bit-exactly
+against torch's own gather; device and host payloads on either side; a
+sender in another process; and the worker methods that replace returning a
+KVobj through Ray (_send_kv_cache / _recv_kv_cache)."""
+import os
+import subprocess
+import sys
+import threading
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from paceserve_amd.core.sequence import Sequence
+from paceserve_amd.kv_transfer import ops
+from paceserve_amd.kv_transfer.channel import KVChannel, KVref
+from paceserve_amd.kv_transfer.kv_utils import KVhelper
+from paceserve_amd.kv_transfer.worker import KVStatus, KVWorker, WorkerSequenceManager
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parent.parent
+_count = [0]
+
+
+def name():
+    _count[0] += 1
+    return f"pace_gpu_test_{os.getpid()}_{_count[0]}"
+
+
+def words(t):
+    return t.view(torch.int16) if t.element_size() == 2 else t.view(torch.uint8)
+
+
+def rand_pool(L, pages, shape, dtype, dev, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return [torch.randn((pages,) + shape, generator=g, device=dev, dtype=torch.float32).to(dtype)
+            for _ in range(L)]
+
+
+def run_pair(slot_bytes, num_slots, send, recv):
+    """Runs send(tx) on a thread and recv(rx) here; returns send's result."""
+    nm = name()
+    rx = KVChannel.create(nm, slot_bytes, num_slots, 4)
+    tx = KVChannel.open(nm, 4, timeout=10)
+    out, errs = [], []
+
+    def sender():
+        try:
+            out.append(send(tx))
+        except Exception as e:                     # reported below
+            errs.append(repr(e))
+
+    t = threading.Thread(target=sender)
+    t.start()
+    try:
+        recv(rx)
+    finally:
+        t.join(timeout=60)
+        tx.close()
+        rx.close()
+    assert not errs, errs
+    return out[0] if out else None
+
+
+# (layers, pool pages, page shape, pages sent, slot bytes): layer chunks, page
+# chunks (a layer larger than a slot), a partial 1 KiB row per page, more
+# layers than one launch takes, one page.
+CASES = [(32, 64, (2, 16, 8, 128), 20, 4 << 20), (4, 300, (2, 16, 8, 128), 200, 1 << 20),
+         (3, 50, (2, 3, 1, 16), 40, 4096), (70, 16, (2, 16, 1, 64), 9, 1 << 20), (2, 8, (2, 16, 8, 128), 1, 1 << 20)]
+
+
+@pytest.mark.parametrize("L,pages,shape,n,slot", CASES)
+def test_device_to_device_through_the_ring(gpu, L, pages, shape, n, slot):
+    print(f"channel case L={L} pages={pages} shape={shape} n={n} slot={slot}", flush=True)
+    src = rand_pool(L, pages, shape, torch.float16, gpu, 1)
+    dst = rand_pool(L, pages, shape, torch.float16, gpu, 2)
+    rng = np.random.default_rng(L + n)
+    s_ids = rng.permutation(pages)[:n].tolist()
+    d_ids = rng.permutation(pages)[:n].tolist()
+    before = [words(d).clone() for d in dst]
+
+    def recv(rx):
+        h = rx.recv_header(timeout=30)
+        assert (h.meta, h.num_layers, h.n_pages) == (b"pages", L, n)
+        rx.recv(dst, d_ids, timeout=30)
+        torch.cuda.synchronize()
+
+    msg = run_pair(slot, 3, lambda tx: tx.send(src, s_ids, b"pages", timeout=30), recv)
+    assert msg >= 1
+    si, di = torch.tensor(s_ids, device=gpu), torch.tensor(d_ids, device=gpu)
+    keep = torch.tensor(sorted(set(range(pages)) - set(d_ids)), device=gpu, dtype=torch.long)
+    for l in range(L):
+        assert torch.equal(words(dst[l])[di], words(src[l])[si]), f"layer {l}"
+        assert torch.equal(words(dst[l])[keep], before[l][keep]), f"layer {l} untouched pages"
+
+
+def test_device_sender_host_receiver_and_back(gpu):
+    L, pages, shape, n = 5, 40, (2, 16, 8, 128), 17
+    src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 3)
+    ids = np.random.default_rng(5).permutation(pages)[:n].tolist()
+    host = torch.empty((L, n) + shape, dtype=torch.bfloat16)
+
+    def recv(rx):
+        rx.recv_header(timeout=30)
+        rx.recv_host(host, timeout=30)
+
+    run_pair(1 << 20, 2, lambda tx: tx.send(src, ids, timeout=30), recv)
+    want = torch.stack([s[torch.tensor(ids, device=gpu)] for s in src]).cpu()
+    assert torch.equal(words(host), words(want))
+
+    dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 4)
+    d_ids = np.random.default_rng(6).permutation(pages)[:n].tolist()
+
+    def recv2(rx):
+        rx.recv_header(timeout=30)
+        rx.recv(dst, d_ids, timeout=30)
+        torch.cuda.synchronize()
+
+    run_pair(1 << 20, 2, lambda tx: tx.send_host(host, timeout=30), recv2)
+    for l in range(L):
+        assert torch.equal(words(dst[l][torch.tensor(d_ids, device=gpu)]).cpu(), words(host[l]))
+
+
+SENDER = r"""
+import sys, torch
+sys.path.insert(0, {root!r})
+from paceserve_amd.kv_transfer.channel import KVChannel
+dev = torch.device("cuda", 0)
+g = torch.Generator(device=dev).manual_seed(77)
+src = [torch.randn((128, 2, 16, 8, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+       for _ in range(32)]
+ch = KVChannel.open({name!r}, 8, timeout=60)
+for r in range(3):
+    ids = list(range(r, 128, 3))[:40]
+    ch.send(src, ids, ("request %d" % r).encode(), timeout=60)
+print("sender done", flush=True)
+ch.close()
+"""
+
+
+def test_sender_in_another_process(gpu):
+    nm = name()
+    rx = KVChannel.create(nm, 16 << 20, 4, 8)
+    child = subprocess.Popen([sys.executable, "-c", SENDER.format(root=str(ROOT), name=nm)])
+    try:
+        g = torch.Generator(device=gpu).manual_seed(77)
+        src = [torch.randn((128, 2, 16, 8, 128), generator=g, device=gpu, dtype=torch.float32).to(torch.bfloat16)
+               for _ in range(32)]
+        dst = [torch.zeros_like(s) for s in src]
+        for r in range(3):
+            h = rx.recv_header(timeout=120)
+            assert h.meta == f"request {r}".encode() and h.n_pages == 40
+            d_ids = list(range(40 * r, 40 * r + 40))
+            rx.recv(dst, d_ids, timeout=60)
+        torch.cuda.synchronize()
+        assert child.wait(timeout=60) == 0
+    finally:
+        if child.poll() is None:
+            child.kill()
+        rx.close()
+    for r in range(3):
+        s_ids = torch.tensor(list(range(r, 128, 3))[:40], device=gpu)
+        d_ids = torch.arange(40 * r, 40 * r + 40, device=gpu)
+        for l in range(32):
+            assert torch.equal(words(dst[l][d_ids]), words(src[l][s_ids])), f"request {r} layer {l}"
+
+
+# ---------------------------------------------------------- worker methods
+
+L, H, D, P, POOL = 4, 8, 128, 16, 64
+
+
+class ModelConfig:
+    dtype = torch.float16
+
+    def get_num_q_heads(self, pc):
+        return 32
+
+    def get_num_kv_heads(self, pc):
+        return H
+
+    def get_head_size(self):
+        return D
+
+    def get_num_layers(self, pc):
+        return L
+
+
+class CacheConfig:
+    block_size = P
+
+
+class _Runner:
+    def __init__(self, cache):
+        self.attention_backend_wrapper = type("W", (), {"gpu_cache": cache})()
+
+
+def make_worker(dev, seed, free_list=None):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    cache = [torch.randn(POOL, 2, P, H, D, generator=g, device=dev, dtype=torch.float32).half() for _ in range(L)]
+    h = KVhelper(0, ModelConfig(), CacheConfig(), None)
+    h.add_model_runner(_Runner(cache))
+    return KVWorker(h, WorkerSequenceManager(P, POOL, free_list=free_list)), cache
+
+
+@pytest.mark.parametrize("tokens_src,tokens_dst", [(40, 40), (48, 49)])
+def test_worker_send_and_receive(gpu, tokens_src, tokens_dst):
+    """prefill side _send_kv_cache (frees the source pages) -> KVref on the
+    control plane -> decode side _recv_kv_cache with LIFO allocation and the
+    n / n+1 remap; the same destination bytes as _get_kv_cache + KVobj +
+    _insert_kv_cache."""
+    src_w, src_cache = make_worker(gpu, 4, np.random.default_rng(4).permutation(POOL).tolist())
+    dst_w, dst_cache = make_worker(gpu, 5)
+    seq = Sequence.of_length("r", tokens_src, P)
+    src_w.seq_manager.add_seq(seq)
+    src_w.seq_manager.block_manager.allocate(seq)
+    src_table = src_w.seq_manager._get_block_table(seq)
+    free_before = src_w.seq_manager.block_manager.get_num_free_gpu_blocks()
+    dst_seq = Sequence.of_length("r", tokens_dst, P)
+    before = [words(c).clone() for c in dst_cache]
+    got = {}
+
+    def recv(rx):
+        got["status"] = dst_w._recv_kv_cache(dst_seq, rx, gpu, timeout=30)
+
+    ref, rank = run_pair(1 << 20, 3, lambda tx: src_w._send_kv_cache(seq, tx, 1.0, 2.0), recv)
+    assert isinstance(ref, KVref) and ref.kv_indices == src_table and rank == 0
+    assert ref.size == L * len(src_table) * 2 * P * H * D * 2 / 1e6
+    assert src_w.seq_manager.block_manager.get_num_free_gpu_blocks() == free_before + len(src_table)
+    st = got["status"]
+    assert isinstance(st, KVStatus) and st.status
+    dst_table = dst_w.seq_manager._get_block_table(dst_seq)
+    n = len(src_table)
+    assert dst_table[:n] == list(range(POOL - 1, POOL - 1 - n, -1))
+    for l in range(L):
+        assert torch.equal(words(dst_cache[l][torch.tensor(dst_table[:n], device=gpu)]),
+                           words(src_cache[l][torch.tensor(src_table, device=gpu)]))
+        untouched = sorted(set(range(POOL)) - set(dst_table[:n]))
+        assert torch.equal(words(dst_cache[l][untouched]), before[l][untouched])
+
+
+def test_worker_receive_refusals_drain_the_message(gpu):
+    """A destination without room, and a message for another sequence, return
+    False and leave the channel ready for the next message."""
+    src_w, src_cache = make_worker(gpu, 6)
+    dst_w, dst_cache = make_worker(gpu, 7, free_list=list(range(3)))          # room for 3 pages
+    seqs = [Sequence.of_length(f"s{i}", 16 * k, P) for i, k in enumerate((5, 2, 2))]
+    for s in seqs:
+        src_w.seq_manager.add_seq(s)
+        src_w.seq_manager.block_manager.allocate(s)
+    tables = [src_w.seq_manager._get_block_table(s) for s in seqs]
+    results = []
+
+    def send(tx):
+        return [src_w._send_kv_cache(s, tx) for s in seqs]
+
+    def recv(rx):
+        results.append(dst_w._recv_kv_cache(Sequence.of_length("s0", 80, P), rx, gpu, timeout=30))   # 5 > 3 pages
+        results.append(dst_w._recv_kv_cache(Sequence.of_length("other", 32, P), rx, gpu, timeout=30))
+        results.append(dst_w._recv_kv_cache(Sequence.of_length("s2", 32, P), rx, gpu, timeout=30))
+        torch.cuda.synchronize()
+
+    run_pair(1 << 20, 2, send, recv)
+    assert results[0] is False and results[1] is False
+    assert isinstance(results[2], KVStatus) and results[2].status
+    dst_table = dst_w.seq_manager._get_block_table(Sequence.of_length("s2", 32, P))
+    for l in range(L):
+        assert torch.equal(words(dst_cache[l][torch.tensor(dst_table, device=gpu)]),
+                           words(src_cache[l][torch.tensor(tables[2], device=gpu)]))
+
+
+def test_helper_zero_fallback_and_repeated_ids(gpu):
+    """A sequence without a block table sends one zero page, as get_kv_cache
+    returns it; repeated destination ids keep the last page written, as the
+    reference's index_put_ does."""
+    src_w, _ = make_worker(gpu, 8)
+    dst_w, dst_cache = make_worker(gpu, 9)
+    src_cache = src_w.kvhelper._gpu_cache()
+
+    class NoTable:
+        def _get_block_table(self, seq):
+            raise KeyError(seq.seq_id)
+
+    class Table:
+        def _get_block_table(self, seq):
+            return [3, 4, 5]
+
+    oks = []
+
+    def send(tx):
+        a = src_w.kvhelper.send_kv_cache(Sequence.of_length("z", 16, P), NoTable(), tx)
+        b = src_w.kvhelper.send_kv_cache(Sequence.of_length("t", 48, P), Table(), tx)
+        return a, b
+
+    def recv(rx):
+        h = rx.recv_header(timeout=30)
+        assert KVref.from_header(h).kv_indices == [0] and h.n_pages == 1
+        oks.append(dst_w.kvhelper.recv_kv_cache(rx, [10], gpu, timeout=30))
+        rx.recv_header(timeout=30)
+        oks.append(dst_w.kvhelper.recv_kv_cache(rx, [20, 21, 20], gpu, timeout=30))
+        torch.cuda.synchronize()
+
+    run_pair(1 << 20, 2, send, recv)
+    assert oks == [True, True]
+    for l in range(L):
+        assert not dst_cache[l][10].any()
+        assert torch.equal(words(dst_cache[l][20]), words(src_cache[l][5]))
+        assert torch.equal(words(dst_cache[l][21]), words(src_cache[l][4]))
