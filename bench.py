@@ -69,6 +69,8 @@ def parse_args():
                     help="skip the pinned-host round trip, also for workloads 3 and 4")
     ap.add_argument("--no-append", action="store_true",
                     help="skip timing the paged-append producer kernel")
+    ap.add_argument("--no-channel", action="store_true",
+                    help="skip timing the cross-process channel (4096-token request between two processes)")
     ap.add_argument("--no-dropin", action="store_true",
                     help="skip timing KVhelper get_kv_cache + insert_kv_cache against the reference's torch "
                          "code for the same calls (4096-token request)")
@@ -494,6 +496,126 @@ def run_dropin(dev, steps: int = 10, warmup: int = 2) -> dict:
     return out
 
 
+# The cross-process channel leg: ring slots and host copy threads per side.
+# Measured on MI355X with 16 host cores for the 512 MiB request: 31-32 GB/s
+# for 16-64 MiB slots and 4-12 threads per side alike (the two DMA passes and
+# two host copies per byte saturate host memory), 24 GB/s with 8 MiB slots.
+CHANNEL_SLOT_BYTES = 32 << 20
+CHANNEL_SLOTS = 4
+CHANNEL_THREADS = 4
+
+
+def channel_sender(name: str) -> None:
+    """The sending process of the channel leg: builds the 4096-token
+    request's source pool (seeded, on the GPU) and sends the request once per
+    line read from stdin, as a prefill instance answers each pull."""
+    import torch
+
+    from paceserve_amd import _native, workloads
+    from paceserve_amd.kv_transfer.channel import KVChannel
+
+    _native.load()
+    dev = torch.device("cuda", 0)
+    w = workloads.get(workloads.PROMOTE)
+    src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev)
+    torch.cuda.synchronize()
+    ids = list(w.src_tables[0])
+    with KVChannel.open(name, CHANNEL_THREADS, timeout=120) as ch:
+        print("ready", flush=True)
+        for line in sys.stdin:
+            ch.send(src, ids, line.strip().encode(), timeout=120)
+
+
+def run_channel(dev, runs: int = 10, warmup: int = 2, ref_runs: int = 3) -> dict:
+    """The 4096-token request moved from another process's cache into this
+    one's through the shared-memory channel: this process asks (a line on the
+    sender's stdin, as a decode instance pulls a sequence), receives the
+    header and unpacks the pages; wall-clock from the ask to the last unpack.
+    Beside it, the reference's path for the same hop, run in this process on
+    a copy of the source pool: get_kv_cache into a pageable tensor
+    (paceserve/kv_transfer/kv_utils.py:44-46), a pickle round trip standing in
+    for the object store (prefill_instance.py:96-107, decode_instance.py:
+    165-171; Ray's RPCs and inter-process copies are left out, so this
+    understates its cost), and insert_kv_cache (:51-52)."""
+    import pickle
+    import subprocess
+
+    import torch
+
+    from paceserve_amd import workloads
+    from paceserve_amd.kv_transfer import ops
+    from paceserve_amd.kv_transfer.channel import KVChannel
+
+    w = workloads.get(workloads.PROMOTE)
+    L, n = w.shape.num_layers, w.n_pages
+    ids = list(w.src_tables[0])
+    dst_ids = list(range(w.dst_pool_pages - 1, w.dst_pool_pages - 1 - n, -1))
+    name = f"pace_bench_{os.getpid()}"
+    ch = KVChannel.create(name, CHANNEL_SLOT_BYTES, CHANNEL_SLOTS, CHANNEL_THREADS)
+    child = subprocess.Popen([sys.executable, str(ROOT / "bench.py"), "--channel-sender", name],
+                             stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True)
+    try:
+        dst = ops.PagedPool(workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev))
+        d_ids = ops.device_ids(dst_ids, dev)
+        if child.stdout.readline().strip() != "ready":
+            raise RuntimeError("channel sender did not start")
+        ts = []
+        for r in range(warmup + runs):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            child.stdin.write(f"{r}\n")
+            child.stdin.flush()
+            h = ch.recv_header(timeout=120)
+            if h.meta != str(r).encode() or h.n_pages != n:
+                raise RuntimeError(f"channel: unexpected message {h}")
+            ch.recv(dst, d_ids, timeout=120)
+            torch.cuda.synchronize()
+            if r >= warmup:
+                ts.append(time.perf_counter() - t0)
+        child.stdin.close()
+        if child.wait(timeout=120) != 0:
+            raise RuntimeError(f"channel sender exited with {child.returncode}")
+    finally:
+        if child.poll() is None:
+            child.kill()
+        ch.close()
+    ms = statistics.median(ts) * 1e3
+    src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev)
+    si, di = torch.tensor(ids, device=dev), torch.tensor(dst_ids, device=dev)
+    ok = all(torch.equal(d[di].view(torch.int16), s[si].view(torch.int16)) for d, s in zip(dst.layers, src))
+    out = {"payload_bytes": w.payload_bytes, "workload": w.name, "runs": runs,
+           "slot_bytes": CHANNEL_SLOT_BYTES, "slots": CHANNEL_SLOTS, "copy_threads_per_side": CHANNEL_THREADS,
+           "channel_ms": round(ms, 2), "channel_gbs": round(w.payload_bytes / (ms / 1e3) / 1e9, 2),
+           "channel_p90_ms": round(sorted(ts)[int(0.9 * (len(ts) - 1))] * 1e3, 2), "same_bytes": ok}
+    log(f"channel: {ms:.2f} ms per request across processes, {out['channel_gbs']} GB/s, same bytes {ok}")
+    del dst
+    torch.cuda.empty_cache()
+    dst = workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev)
+    rts = []
+    for r in range(1 + ref_runs):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        seq_cache = torch.zeros((L, n) + w.shape.page_shape, dtype=w.shape.dtype)
+        for i in range(L):
+            seq_cache[i] = src[i][torch.tensor(ids), :, :, :, :]
+        got = pickle.loads(pickle.dumps(seq_cache))
+        for i in range(L):
+            dst[i][torch.tensor(dst_ids), :, :, :, :] = got[i].to(dev)
+        torch.cuda.synchronize()
+        if r >= 1:
+            rts.append(time.perf_counter() - t0)
+    rms = statistics.median(rts) * 1e3
+    out["reference_emulated_ms"] = round(rms, 2)
+    out["reference_emulated_gbs"] = round(w.payload_bytes / (rms / 1e3) / 1e9, 2)
+    out["reference_emulated"] = ("get_kv_cache (pageable, per layer) + pickle.dumps/loads + insert_kv_cache "
+                                 "(per layer), one process; excludes Ray's RPCs and object-store copies")
+    out["speedup_vs_reference_emulated"] = round(rms / ms, 2)
+    log(f"channel reference path (emulated): {rms:.2f} ms")
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
 def link_settle(dev, target_gbs: float = 45.0, max_wait_s: float = 30.0, streak: int = 3) -> dict:
     """Waits until `streak` consecutive 64 MiB pinned device-to-host copies,
     0.2 s apart, each run at target_gbs or more (other DMA work, such as the
@@ -879,7 +1001,7 @@ def pmc_markdown(traffic_json: str) -> str:
     # one launch reads and writes its layer chunk's pages once
     chunk = min(w.device_layers_per_chunk or w.shape.num_layers, w.shape.num_layers)
     alg = 2 * chunk * w.n_pages * w.shape.page_bytes
-    run = (f"python3 bench.py --workload {wl} --no-cpu --no-promote --no-staging --no-dropin --no-append "
+    run = (f"python3 bench.py --workload {wl} --no-cpu --no-promote --no-staging --no-dropin --no-append --no-channel "
            "--steps 3 --warmup 1 --calibrate")
     cmds = [
         "export TMPDIR=/tmp",
@@ -918,6 +1040,10 @@ def traffic_from_profiles(workload: str):
 
 
 def main():
+    if len(sys.argv) > 2 and sys.argv[1] == "--channel-sender":
+        # the sending process of the channel leg (started by run_channel)
+        channel_sender(sys.argv[2])
+        return
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-pmc":
         # python bench.py --summarize-pmc FETCH.csv WRITE.csv WORKLOAD
         d = summarize_pmc(sys.argv[2], sys.argv[3], sys.argv[4])
@@ -991,6 +1117,11 @@ def main():
         dropin["link_probe"] = settle
     del src, dst, s_ids, d_ids
     torch.cuda.empty_cache()
+    channel = None
+    if not args.no_channel:
+        settle = link_settle(dev)
+        channel = run_channel(dev)
+        channel["link_probe"] = settle
 
     line = {
         "metric": METRIC,
@@ -1018,6 +1149,7 @@ def main():
         "promote_4k": promote,
         "staging": staging,
         "dropin": dropin,
+        "channel": channel,
         "cpu_baseline": cpu,
     }
     tr = traffic_from_profiles(w.name) if args.mode == "buffer" else None

@@ -63,15 +63,15 @@ class KVChannel:
         self._inflight: list = []
 
     @classmethod
-    def create(cls, name: str, slot_bytes: int = 64 * MiB, num_slots: int = 4,
-               copy_threads: int = 8) -> "KVChannel":
+    def create(cls, name: str, slot_bytes: int = 32 * MiB, num_slots: int = 4,
+               copy_threads: int = 4) -> "KVChannel":
         handle = ctypes.c_void_p()
         _native.check(_native.load().pace_kv_channel_create(name.encode(), int(slot_bytes), int(num_slots),
                                                             int(copy_threads), ctypes.byref(handle)))
         return cls(handle.value, name)
 
     @classmethod
-    def open(cls, name: str, copy_threads: int = 8, timeout: float = 30.0) -> "KVChannel":
+    def open(cls, name: str, copy_threads: int = 4, timeout: float = 30.0) -> "KVChannel":
         handle = ctypes.c_void_p()
         _native.check(_native.load().pace_kv_channel_open(name.encode(), int(copy_threads), _ms(timeout),
                                                           ctypes.byref(handle)))
