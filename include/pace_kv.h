@@ -361,7 +361,8 @@ int pace_kv_promote(pace_kv_promoter* promoter, pace_kv_allocator* dst_alloc,
  * One sender and one receiver per channel; each endpoint serialises its own
  * sends (whole messages) and its own receives.  Every blocking call waits at
  * most timeout_ms milliseconds (PACE_KV_ETIMEDOUT; 0 = do not wait) and
- * returns PACE_KV_ECLOSED once either side has closed the channel.  A sender
+ * returns PACE_KV_ECLOSED once either side has closed the channel or the peer
+ * process has exited (checked at least every 10 ms while waiting).  A sender
  * that fails after the header marks the message abandoned, and the
  * receiver's next wait for its chunks fails with PACE_KV_ESTATE.
  *

@@ -22,6 +22,8 @@
 // then uploads it and unpacks it while the next chunk is copied.
 #include <errno.h>
 #include <fcntl.h>
+#include <signal.h>
+#include <stdio.h>
 #include <linux/futex.h>
 #include <string.h>
 #include <sys/mman.h>
@@ -46,7 +48,7 @@ using pace_kv::hip_status;
 namespace {
 
 constexpr uint64_t kMagic = 0x50414345'4b564348ull;  // "PACEKVCH"
-constexpr uint32_t kVersion = 1;
+constexpr uint32_t kVersion = 2;
 constexpr int kMaxSlots = 64;
 constexpr int kNameMax = 200;
 
@@ -68,6 +70,15 @@ struct alignas(64) SlotRecord {
   int32_t pad;
 };
 
+// Which process plays a role (sender or receiver): its pid, its pid
+// namespace and its start time, so that a waiting peer can tell that the
+// process has exited (or that its pid now names another process).
+struct ProcessId {
+  std::atomic<int32_t> pid;      // 0: no process has taken the role yet
+  std::atomic<uint64_t> pidns;   // inode of /proc/<pid>/ns/pid
+  std::atomic<uint64_t> start;   // start time, field 22 of /proc/<pid>/stat
+};
+
 struct alignas(64) ChannelCtl {
   uint64_t magic;
   uint32_t version;
@@ -80,10 +91,71 @@ struct alignas(64) ChannelCtl {
   alignas(64) std::atomic<uint32_t> closed;  // either side closed the channel
   std::atomic<uint64_t> next_msg_id;         // sender: id of the next message
   std::atomic<uint64_t> aborted_msg;         // sender: id of a message it gave up (0 = none)
+  ProcessId sender, receiver;
   SlotRecord slots[kMaxSlots];
 };
 
 int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+// State (field 3) and start time (field 22) of /proc/<pid>/stat; false if the
+// process does not exist.
+bool proc_stat(int pid, char* state, uint64_t* start) {
+  char path[64];
+  snprintf(path, sizeof(path), "/proc/%d/stat", pid);
+  FILE* f = fopen(path, "r");
+  if (f == nullptr) return false;
+  char buf[1024];
+  const size_t n = fread(buf, 1, sizeof(buf) - 1, f);
+  fclose(f);
+  buf[n] = '\0';
+  const char* p = strrchr(buf, ')');  // the command name may hold spaces
+  if (p == nullptr) return false;
+  unsigned long long st = 0;
+  // after ") ": state, then 18 fields, then the start time
+  if (sscanf(p + 2, "%c %*s %*s %*s %*s %*s %*s %*s %*s %*s %*s %*s %*s %*s %*s %*s %*s %*s %*s %llu",
+             state, &st) != 2)
+    return false;
+  *start = st;
+  return true;
+}
+
+uint64_t pid_namespace(const char* who) {
+  char path[64];
+  snprintf(path, sizeof(path), "/proc/%s/ns/pid", who);
+  struct stat st;
+  return stat(path, &st) == 0 ? static_cast<uint64_t>(st.st_ino) : 0;
+}
+
+// Records the calling process as the one playing `role`.
+void take_role(ProcessId& role) {
+  static const int32_t pid = static_cast<int32_t>(getpid());
+  static const uint64_t ns = pid_namespace("self");
+  static const uint64_t start = [] {
+    char state = 0;
+    uint64_t t = 0;
+    return proc_stat(static_cast<int>(getpid()), &state, &t) ? t : 0;
+  }();
+  if (role.pid.load(std::memory_order_acquire) == pid) return;
+  role.pid.store(0, std::memory_order_release);
+  role.pidns.store(ns, std::memory_order_relaxed);
+  role.start.store(start, std::memory_order_relaxed);
+  role.pid.store(pid, std::memory_order_release);
+}
+
+// True when the process recorded in `role` is known to have exited.  A role
+// not yet taken, taken by this process, or taken in another pid namespace
+// (whose pids this process cannot check) counts as alive.
+bool role_gone(const ProcessId& role) {
+  const int32_t pid = role.pid.load(std::memory_order_acquire);
+  if (pid <= 0 || pid == static_cast<int32_t>(getpid())) return false;
+  static const uint64_t own_ns = pid_namespace("self");
+  if (own_ns == 0 || role.pidns.load(std::memory_order_relaxed) != own_ns) return false;
+  if (kill(pid, 0) != 0 && errno == ESRCH) return true;
+  char state = 0;
+  uint64_t start = 0;
+  if (!proc_stat(pid, &state, &start)) return false;  // cannot tell
+  return state == 'Z' || state == 'X' || start != role.start.load(std::memory_order_relaxed);
+}
 
 long futex(std::atomic<uint32_t>* word, int op, uint32_t val, const timespec* ts) {
   return syscall(SYS_futex, reinterpret_cast<uint32_t*>(word), op, val, ts, nullptr, 0);
@@ -284,10 +356,12 @@ char* slot_data(pace_kv_channel* ch, uint32_t idx) {
 }
 
 // Waits until cond() holds.  `word` is the futex word the other side bumps
-// when it may have made cond() true; closing the channel also wakes it.
+// when it may have made cond() true; closing the channel also wakes it.  The
+// peer process is checked at every wake-up (at least every 10 ms), so a wait
+// on a peer that died ends then rather than at the deadline.
 template <class Cond>
-int wait_for(pace_kv_channel* ch, std::atomic<uint32_t>* word, Cond cond, int timeout_ms,
-             const char* what) {
+int wait_for(pace_kv_channel* ch, std::atomic<uint32_t>* word, const ProcessId& peer, Cond cond,
+             int timeout_ms, const char* what) {
   using clock = std::chrono::steady_clock;
   const auto deadline = clock::now() + std::chrono::milliseconds(timeout_ms < 0 ? 0 : timeout_ms);
   for (int spin = 0;; ++spin) {
@@ -299,6 +373,9 @@ int wait_for(pace_kv_channel* ch, std::atomic<uint32_t>* word, Cond cond, int ti
       __builtin_ia32_pause();
       continue;
     }
+    if (role_gone(peer))
+      return fail(PACE_KV_ECLOSED, "channel %s: the peer process %d exited while this side waited for %s",
+                  ch->name.c_str(), peer.pid.load(), what);
     const auto left = std::chrono::duration_cast<std::chrono::microseconds>(deadline - clock::now()).count();
     if (left <= 0)
       return fail(PACE_KV_ETIMEDOUT, "channel %s: timed out after %d ms waiting for %s", ch->name.c_str(),
@@ -313,7 +390,7 @@ int wait_for(pace_kv_channel* ch, std::atomic<uint32_t>* word, Cond cond, int ti
 int acquire_slot(pace_kv_channel* ch, int timeout_ms, uint32_t* idx) {
   ChannelCtl* c = ch->ctl;
   const uint32_t h = c->head.load(std::memory_order_relaxed);
-  PACE_KV_TRY(wait_for(ch, &c->tail,
+  PACE_KV_TRY(wait_for(ch, &c->tail, c->receiver,
                        [&] { return h - c->tail.load(std::memory_order_acquire) < c->num_slots; },
                        timeout_ms, "a free slot"));
   *idx = h % c->num_slots;
@@ -329,10 +406,11 @@ void publish(pace_kv_channel* ch) {
 // Receiver: waits for the next record and returns its slot index.
 int next_record(pace_kv_channel* ch, int timeout_ms, uint32_t* idx, const char* what) {
   ChannelCtl* c = ch->ctl;
+  take_role(c->receiver);
   const uint32_t t = c->tail.load(std::memory_order_relaxed);
   const uint64_t msg = ch->rx_msg;
   const bool active = ch->rx_active;
-  PACE_KV_TRY(wait_for(ch, &c->head,
+  PACE_KV_TRY(wait_for(ch, &c->head, c->sender,
                        [&] {
                          return c->head.load(std::memory_order_acquire) != t ||
                                 (active && c->aborted_msg.load(std::memory_order_acquire) == msg);
@@ -437,6 +515,7 @@ int staging_ready(pace_kv_channel* ch, Staging& s) {
 int send_header(pace_kv_channel* ch, int num_layers, int64_t n_pages, int64_t page_bytes, const void* meta,
                 int64_t meta_bytes, int timeout_ms, uint64_t* msg_id) {
   ChannelCtl* c = ch->ctl;
+  take_role(c->sender);
   if (meta_bytes < 0 || (meta_bytes > 0 && meta == nullptr))
     return fail(PACE_KV_EINVAL, "channel: bad metadata");
   if (meta_bytes > c->slot_bytes)
@@ -570,6 +649,11 @@ int pace_kv_channel_create(const char* name, int64_t slot_bytes, int num_slots, 
   c->closed.store(0);
   c->next_msg_id.store(0);
   c->aborted_msg.store(0);
+  for (ProcessId* r : {&c->sender, &c->receiver}) {
+    r->pid.store(0);
+    r->pidns.store(0);
+    r->start.store(0);
+  }
   std::atomic_thread_fence(std::memory_order_release);
   // The magic goes in last: an opener that sees it sees a complete block.
   __atomic_store_n(&c->magic, kMagic, __ATOMIC_RELEASE);

@@ -1,7 +1,8 @@
 """The cross-process channel's protocol on host payloads (no GPU): messages in
 order with their metadata, payloads larger than the ring streaming through
 it, layer- and page-sized chunks, another process as the sender, deadlines,
-closing, abandoned messages, draining, and argument errors."""
+closing, abandoned messages, draining, a peer process that dies mid-message,
+and argument errors."""
 import os
 import subprocess
 import sys
@@ -268,3 +269,70 @@ def test_kvref_round_trips_the_kvobj_fields():
     b = KVref.from_header(h)
     assert (b.seq_id, b.kv_indices, b.size, b.left_prefill, b.kv_transfer_start, b.msg_id) == \
         (17, [5, 3, 9], 2.25, 1.0, 2.0, 42)
+
+
+STALLED_SENDER = r"""
+import sys, torch
+sys.path.insert(0, {root!r})
+from paceserve_amd.kv_transfer.channel import KVChannel
+ch = KVChannel.open({name!r}, 1, timeout=30)
+ch.send_host(torch.zeros((2, 64, 2, 4, 1, 16), dtype=torch.float16), b"big", timeout=120)
+"""
+
+STALLED_RECEIVER = r"""
+import sys, time
+sys.path.insert(0, {root!r})
+from paceserve_amd.kv_transfer.channel import KVChannel
+ch = KVChannel.open({name!r}, 1, timeout=30)
+ch.recv_header(timeout=120)
+print("got", flush=True)
+time.sleep(120)
+"""
+
+
+def test_a_dead_sender_ends_the_receivers_wait():
+    nm = name()
+    rx = KVChannel.create(nm, 4096, 2, 1)
+    child = subprocess.Popen([sys.executable, "-c", STALLED_SENDER.format(root=str(ROOT), name=nm)])
+    try:
+        h = rx.recv_header(timeout=60)
+        assert h.meta == b"big"
+        child.kill()                                  # a zombie until reaped: still counts as exited
+        t0 = time.monotonic()
+        with pytest.raises(_native.PaceKVError) as e:
+            rx.recv_host(torch.empty((2, 64, 2, 4, 1, 16), dtype=torch.float16), timeout=60)
+        assert status(e) == _native.PACE_KV_ECLOSED and "exited" in str(e.value)
+        assert time.monotonic() - t0 < 5
+    finally:
+        child.kill()
+        child.wait()
+        rx.close()
+
+
+def test_a_dead_receiver_ends_the_senders_wait():
+    nm = name()
+    tx = KVChannel.create(nm, 4096, 2, 1)
+    child = subprocess.Popen([sys.executable, "-c", STALLED_RECEIVER.format(root=str(ROOT), name=nm)],
+                             stdout=subprocess.PIPE, text=True)
+    errs = []
+
+    def send():
+        try:
+            tx.send_host(torch.zeros((2, 64, 2, 4, 1, 16), dtype=torch.float16), b"big", timeout=60)
+        except _native.PaceKVError as exc:
+            errs.append(exc)
+
+    t = threading.Thread(target=send)
+    try:
+        t.start()
+        assert child.stdout.readline().strip() == "got"
+        t0 = time.monotonic()
+        child.kill()
+        t.join(timeout=30)
+        assert len(errs) == 1 and errs[0].status == _native.PACE_KV_ECLOSED and "exited" in str(errs[0])
+        assert time.monotonic() - t0 < 5
+    finally:
+        child.kill()
+        child.wait()
+        t.join(timeout=30)
+        tx.close()
