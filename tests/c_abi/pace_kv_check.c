@@ -3,18 +3,23 @@
  * no torch.  Allocates two 3-layer pools with the HIP runtime, packs four
  * pages of the source pool into a transfer buffer, unpacks them into other
  * pages of the destination pool, and checks every byte on the host against a
- * plain memcpy restatement.  Also checks that an argument error returns
- * PACE_KV_EINVAL with a message.  Exit status 0 means every check passed.
+ * plain memcpy restatement.  Then sends four pages through a cross-process
+ * channel (both endpoints in this process: the message fits the ring) into
+ * further destination pages, and checks them the same way.  Also checks that
+ * an argument error returns PACE_KV_EINVAL with a message.  Exit status 0
+ * means every check passed.
  *
  * Build (the package build does this): gcc -std=c99 -D__HIP_PLATFORM_AMD__
  *   -I/opt/rocm/include -Iinclude pace_kv_check.c -Lpaceserve_amd -lpace_kv
  *   -L/opt/rocm/lib -lamdhip64
  */
+#define _POSIX_C_SOURCE 200809L
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 #include "pace_kv.h"
 
@@ -40,11 +45,12 @@ int main(void) {
   const size_t pool_bytes = (size_t)POOL_PAGES * PAGE_BYTES;
   const int32_t src_ids[N] = {5, 0, 11, 3};
   const int32_t dst_ids[N] = {2, 9, 14, 7};
+  const int32_t ch_ids[N] = {12, 1, 4, 8};    /* destination pages of the channel message */
   unsigned char* host_src[LAYERS];
   unsigned char* host_dst[LAYERS];
   void* src_layers[LAYERS];
   void* dst_layers[LAYERS];
-  void *buf, *ids_src, *ids_dst;
+  void *buf, *ids_src, *ids_dst, *ids_ch;
   unsigned char* host_buf = malloc((size_t)LAYERS * N * PAGE_BYTES);
   unsigned char* got = malloc(pool_bytes);
   int l, j, p, failures = 0;
@@ -68,6 +74,8 @@ int main(void) {
   HIP_OK(hipMalloc(&buf, (size_t)LAYERS * N * PAGE_BYTES));
   HIP_OK(hipMalloc(&ids_src, sizeof(src_ids)));
   HIP_OK(hipMalloc(&ids_dst, sizeof(dst_ids)));
+  HIP_OK(hipMalloc(&ids_ch, sizeof(ch_ids)));
+  HIP_OK(hipMemcpy(ids_ch, ch_ids, sizeof(ch_ids), hipMemcpyHostToDevice));
   HIP_OK(hipMemcpy(ids_src, src_ids, sizeof(src_ids), hipMemcpyHostToDevice));
   HIP_OK(hipMemcpy(ids_dst, dst_ids, sizeof(dst_ids), hipMemcpyHostToDevice));
 
@@ -113,6 +121,50 @@ int main(void) {
     }
   }
 
+  /* the same pages through a channel: src[l][src_ids[j]] -> dst[l][ch_ids[j]] */
+  {
+    char name[64], meta[16];
+    pace_kv_channel *rx = NULL, *tx = NULL;
+    uint64_t sent = 0, got_id = 0;
+    int64_t meta_len = 0, n_pages = 0, page_bytes = 0;
+    int num_layers = 0;
+    snprintf(name, sizeof(name), "pace_c_check_%d", (int)getpid());
+    rc = pace_kv_channel_create(name, 65536, 4, 2, &rx);
+    if (rc == PACE_KV_OK) rc = pace_kv_channel_open(name, 2, 1000, &tx);
+    if (rc == PACE_KV_OK)
+      rc = pace_kv_channel_send(tx, (const void* const*)src_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_src, N,
+                                PAGE_BYTES, "four", 4, 1000, &sent, NULL);
+    if (rc == PACE_KV_OK)
+      rc = pace_kv_channel_recv_header(rx, meta, sizeof(meta), &meta_len, &num_layers, &n_pages, &page_bytes,
+                                       &got_id, 1000);
+    if (rc == PACE_KV_OK &&
+        (meta_len != 4 || memcmp(meta, "four", 4) != 0 || num_layers != LAYERS || n_pages != N ||
+         page_bytes != PAGE_BYTES || got_id != sent)) {
+      fprintf(stderr, "channel header differs\n");
+      ++failures;
+    }
+    if (rc == PACE_KV_OK)
+      rc = pace_kv_channel_recv(rx, dst_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_ch, N, PAGE_BYTES, NULL,
+                                1000, NULL);
+    if (rc != PACE_KV_OK) {
+      fprintf(stderr, "channel status %d: %s\n", rc, pace_kv_last_error());
+      return 1;
+    }
+    HIP_OK(hipDeviceSynchronize());
+    pace_kv_channel_close(tx);
+    pace_kv_channel_close(rx);
+    for (l = 0; l < LAYERS; ++l) {
+      for (j = 0; j < N; ++j)
+        memcpy(host_dst[l] + (size_t)ch_ids[j] * PAGE_BYTES, host_src[l] + (size_t)src_ids[j] * PAGE_BYTES,
+               PAGE_BYTES);
+      HIP_OK(hipMemcpy(got, dst_layers[l], pool_bytes, hipMemcpyDeviceToHost));
+      if (memcmp(got, host_dst[l], pool_bytes) != 0) {
+        fprintf(stderr, "destination layer %d differs after the channel message\n", l);
+        ++failures;
+      }
+    }
+  }
+
   /* an argument error is caught on the host, before any launch */
   rc = pace_kv_pack((const void* const*)src_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_src, N, 100,
                     buf, (int64_t)N * PAGE_BYTES, NULL, NULL);
@@ -130,10 +182,11 @@ int main(void) {
   HIP_OK(hipFree(buf));
   HIP_OK(hipFree(ids_src));
   HIP_OK(hipFree(ids_dst));
+  HIP_OK(hipFree(ids_ch));
   free(host_buf);
   free(got);
   if (failures) return 1;
-  printf("pace_kv C ABI check passed: %d layers x %d pages of %d B packed and unpacked\n", LAYERS, N,
-         PAGE_BYTES);
+  printf("pace_kv C ABI check passed: %d layers x %d pages of %d B packed and unpacked, and sent through "
+         "a channel\n", LAYERS, N, PAGE_BYTES);
   return 0;
 }
