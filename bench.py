@@ -273,7 +273,27 @@ def run_ceiling(w, dev, src, dst, n: int, reps: int = 10) -> dict:
     torch.cuda.synchronize()
     gbs = 4 * w.payload_bytes * reps / (a.elapsed_time(b) / 1e3) / 1e9
     log(f"contiguous ceiling (identity ids): {gbs:.1f} GB/s")
-    return {"identity_ids_gbs": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    # The runtime's own device copy (torch copy_ -> hipMemcpyAsync, a blit
+    # kernel) of one launch's payload, between 1 GiB (smaller copies repeated
+    # on the same buffers stay in the 256 MB memory-side cache) and 4 GiB: an
+    # outside reference for what a contiguous copy reaches on this device.
+    nbytes = max(1 << 30, min(min(k, L) * n * w.shape.page_bytes, 4 << 30))
+    del buf
+    x = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(reps):
+        y.copy_(x)
+    b.record(stream)
+    torch.cuda.synchronize()
+    runtime = 2 * nbytes * reps / (a.elapsed_time(b) / 1e3) / 1e9
+    log(f"runtime device copy of {nbytes} B: {runtime:.1f} GB/s")
+    del x, y
+    return {"identity_ids_gbs": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "runtime_copy_gbs": round(runtime, 1), "runtime_copy_bytes": nbytes,
+            "runtime_copy": "torch copy_ of one contiguous buffer (hipMemcpyAsync device to device)"}
 
 
 def run_torch_device(w, dev, src, dst, s_ids, d_ids, reps: int = 3) -> dict:
