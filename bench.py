@@ -804,10 +804,10 @@ def run_calibration(dev) -> None:
     a = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
     b = torch.empty_like(a)
     torch.cuda.synchronize()
-    for _ in range(3):
+    for _ in range(CALIBRATION_COPIES):
         b.copy_(a)
     torch.cuda.synchronize()
-    log("calibration: 3 x 1 GiB torch copy_ done")
+    log(f"calibration: {CALIBRATION_COPIES} x 1 GiB torch copy_ done")
 
 
 def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan):
@@ -866,11 +866,15 @@ def _json(path: str) -> dict:
 KERNEL_TAG = "page_copy_kernel<false, false, true>"
 
 
+# Copies of 1 GiB that --calibrate runs last in a bench run.
+CALIBRATION_COPIES = 3
+
+
 def _per_dispatch(csv_path: str, counter: str):
+    """Counter values per kernel name, in dispatch order."""
     by = {}
-    for r in _rows(csv_path):
-        if r["Counter_Name"] != counter:
-            continue
+    rows = [r for r in _rows(csv_path) if r["Counter_Name"] == counter]
+    for r in sorted(rows, key=lambda r: int(r["Dispatch_Id"])):
         by.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
     return by
 
@@ -879,9 +883,11 @@ def summarize_pmc(fetch_csv: str, write_csv: str, workload: str) -> dict:
     """HBM bytes per copy-kernel launch from two rocprofv3 --pmc runs
     (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled so that the 1 GiB
     device copy run by --calibrate (dispatched as __amd_rocclr_copyBuffer)
-    reads 1 GiB fetched and 1 GiB written."""
+    reads 1 GiB fetched and 1 GiB written.  The calibration copies are the
+    run's last CALIBRATION_COPIES large copy dispatches: earlier ones (the
+    runtime copy beside the copy ceiling) have other sizes."""
     gib_kib = float(1 << 20)
-    out = {"workload": workload, "kernel": KERNEL_TAG}
+    out = {"workload": workload, "kernel": KERNEL_TAG, "fetch_csv": fetch_csv, "write_csv": write_csv}
     for name, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"), ("write", write_csv, "WRITE_SIZE")):
         by = _per_dispatch(path, counter)
         names = sorted({k.replace("void pace_kv::(anonymous namespace)::", "").split("(")[0]
@@ -890,6 +896,7 @@ def summarize_pmc(fetch_csv: str, write_csv: str, workload: str) -> dict:
             out["kernel"] = " and ".join(names)
         ours = [v for k, vals in by.items() if "page_copy_kernel" in k for v in vals]
         calib = [v for k, vals in by.items() if "copyBuffer" in k for v in vals if v > 0.25 * gib_kib]
+        calib = calib[-CALIBRATION_COPIES:]
         if not ours or not calib:
             raise SystemExit(f"{path}: missing page_copy_kernel or calibration dispatches")
         factor = gib_kib / statistics.mean(calib)
@@ -1023,12 +1030,16 @@ def pmc_markdown(traffic_json: str) -> str:
     alg = 2 * chunk * w.n_pages * w.shape.page_bytes
     run = (f"python3 bench.py --workload {wl} --no-cpu --no-promote --no-staging --no-dropin --no-append --no-channel "
            "--steps 3 --warmup 1 --calibrate")
+    # the counter runs wrote their CSVs (<dir>/f_counter_collection.csv and
+    # <dir>/w_counter_collection.csv) where the summary read them
+    fdir = os.path.dirname(t.get("fetch_csv", f"pmc_fetch_{wl}/f_counter_collection.csv"))
+    wdir = os.path.dirname(t.get("write_csv", f"pmc_write_{wl}/w_counter_collection.csv"))
     cmds = [
         "export TMPDIR=/tmp",
-        f"timeout -s KILL 300 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch_{wl} -o f -- {run}",
-        f"timeout -s KILL 300 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write_{wl} -o w -- {run}",
-        f"python3 bench.py --summarize-pmc gpurun_out/pmc_fetch_{wl}/f_counter_collection.csv "
-        f"gpurun_out/pmc_write_{wl}/w_counter_collection.csv {wl} > profiles/page_copy_{wl}_traffic.json",
+        f"timeout -s KILL 300 rocprofv3 --pmc FETCH_SIZE --output-format csv -d {fdir} -o f -- {run}",
+        f"timeout -s KILL 300 rocprofv3 --pmc WRITE_SIZE --output-format csv -d {wdir} -o w -- {run}",
+        f"python3 bench.py --summarize-pmc {fdir}/f_counter_collection.csv "
+        f"{wdir}/w_counter_collection.csv {wl} > profiles/page_copy_{wl}_traffic.json",
         f"python3 bench.py --pmc-markdown profiles/page_copy_{wl}_traffic.json > profiles/page_copy_{wl}_traffic.md",
     ]
     out = [f"# {t['kernel']} on {wl} - HBM traffic per launch (rocprofv3 PMC)", "",

@@ -39,14 +39,16 @@ def test_copy_kernel_names_follow_the_store_policy():
 def test_summarize_pmc_scales_counters_by_the_calibration_copy(tmp_path):
     gib_kib = float(1 << 20)
     # FETCH_SIZE reads half of the true bytes, WRITE_SIZE all of them: the
-    # calibration copy of 1 GiB shows it and the factors undo it.
-    fetch = [{"Kernel_Name": COPY, "Counter_Name": "FETCH_SIZE", "Counter_Value": 1000.0},
-             {"Kernel_Name": COPY_T, "Counter_Name": "FETCH_SIZE", "Counter_Value": 1000.0},
-             {"Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": "FETCH_SIZE", "Counter_Value": gib_kib / 2},
-             {"Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": "FETCH_SIZE", "Counter_Value": 4.0}]
-    write = [{"Kernel_Name": COPY, "Counter_Name": "WRITE_SIZE", "Counter_Value": 2000.0},
-             {"Kernel_Name": COPY_T, "Counter_Name": "WRITE_SIZE", "Counter_Value": 2000.0},
-             {"Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": "WRITE_SIZE", "Counter_Value": gib_kib}]
+    # calibration copies of 1 GiB (the run's last three large copies) show it
+    # and the factors undo it.  A 4 GiB copy earlier in the run and a 4 KiB
+    # copy are not calibrations.
+    cb = "__amd_rocclr_copyBuffer"
+    fetch = [(COPY, 1000.0), (cb, 4 * gib_kib / 2), (COPY_T, 1000.0), (cb, 4.0)] + [(cb, gib_kib / 2)] * 3
+    write = [(COPY, 2000.0), (cb, 4 * gib_kib), (COPY_T, 2000.0)] + [(cb, gib_kib)] * 3
+    fetch = [{"Dispatch_Id": i + 1, "Kernel_Name": k, "Counter_Name": "FETCH_SIZE", "Counter_Value": v}
+             for i, (k, v) in enumerate(fetch)]
+    write = [{"Dispatch_Id": i + 1, "Kernel_Name": k, "Counter_Name": "WRITE_SIZE", "Counter_Value": v}
+             for i, (k, v) in enumerate(write)]
     d = bench.summarize_pmc(write_csv(tmp_path / "f.csv", fetch), write_csv(tmp_path / "w.csv", write), "llama3-8b-512tok-fp16")
     assert d["fetch_scale"] == 2.0 and d["write_scale"] == 1.0     # the 4 KiB copy is not a calibration
     assert d["fetch_bytes_per_launch"] == 2000 * 1024
@@ -57,7 +59,7 @@ def test_summarize_pmc_scales_counters_by_the_calibration_copy(tmp_path):
 
 
 def test_summarize_pmc_needs_both_kinds_of_dispatch(tmp_path):
-    rows = [{"Kernel_Name": COPY, "Counter_Name": "FETCH_SIZE", "Counter_Value": 1.0}]
+    rows = [{"Dispatch_Id": 1, "Kernel_Name": COPY, "Counter_Name": "FETCH_SIZE", "Counter_Value": 1.0}]
     path = write_csv(tmp_path / "f.csv", rows)
     with pytest.raises(SystemExit):
         bench.summarize_pmc(path, path, "llama3-8b-16req-bf16")
