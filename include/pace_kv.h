@@ -388,6 +388,10 @@ int pace_kv_channel_open(const char* name, int copy_threads, int timeout_ms,
 int pace_kv_channel_close(pace_kv_channel* channel);
 int pace_kv_channel_info(pace_kv_channel* channel, int64_t* slot_bytes,
                          int* num_slots);
+/* Removes the name "/<name>" (a channel left behind by a creator that died
+ * before closing it); endpoints already open keep working.  A name that does
+ * not exist is not an error. */
+int pace_kv_channel_unlink(const char* name);
 
 /* Sends one message whose payload is packed from device pools:
  *   payload[l][j] = src_layers[l][page_ids[j]] (page_ids: device int32).

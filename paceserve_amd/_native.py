@@ -65,6 +65,7 @@ SIGNATURES = {
     "pace_kv_channel_open": (c_int, [c_char_p, c_int, c_int, POINTER(c_void_p)]),
     "pace_kv_channel_close": (c_int, [_VP]),
     "pace_kv_channel_info": (c_int, [_VP, POINTER(c_int64), POINTER(c_int)]),
+    "pace_kv_channel_unlink": (c_int, [c_char_p]),
     "pace_kv_channel_send": (
         c_int, [_VP, _VP, c_int, c_int64, _VP, c_int64, c_int64, _VP, c_int64, c_int, POINTER(c_uint64), _VP]),
     "pace_kv_channel_send_host": (

@@ -465,8 +465,18 @@ void destroy(pace_kv_channel* ch) {
   free_staging(ch->rx);
   delete ch->pool;
   if (ch->base) munmap(ch->base, static_cast<size_t>(ch->map_bytes));
+  if (ch->creator && ch->fd >= 0) {
+    // The name is removed only while it still names this channel's object:
+    // after an unlink and a new create under the same name it names another.
+    const std::string shm_name = "/" + ch->name;
+    const int cur = shm_open(shm_name.c_str(), O_RDONLY, 0);
+    struct stat mine, now;
+    if (cur >= 0 && fstat(ch->fd, &mine) == 0 && fstat(cur, &now) == 0 && mine.st_ino == now.st_ino &&
+        mine.st_dev == now.st_dev)
+      shm_unlink(shm_name.c_str());
+    if (cur >= 0) close(cur);
+  }
   if (ch->fd >= 0) close(ch->fd);
-  if (ch->creator) shm_unlink(("/" + ch->name).c_str());
   delete ch;
 }
 
@@ -712,6 +722,13 @@ int pace_kv_channel_close(pace_kv_channel* ch) {
     for (int i = 0; i < 2; ++i) (void)hipEventSynchronize(s->drained[i]);
   }
   destroy(ch);
+  return PACE_KV_OK;
+}
+
+int pace_kv_channel_unlink(const char* name) {
+  PACE_KV_TRY(check_name(name));
+  if (shm_unlink(("/" + std::string(name)).c_str()) != 0 && errno != ENOENT)
+    return fail(PACE_KV_EINVAL, "channel %s: shm_unlink failed: %s", name, strerror(errno));
   return PACE_KV_OK;
 }
 

@@ -77,6 +77,12 @@ class KVChannel:
                                                           ctypes.byref(handle)))
         return cls(handle.value, name)
 
+    @staticmethod
+    def unlink(name: str) -> None:
+        """Removes a channel name left behind by a creator that died without
+        closing it (open endpoints keep working)."""
+        _native.check(_native.load().pace_kv_channel_unlink(name.encode()))
+
     def _require(self) -> int:
         if self._handle is None:
             raise RuntimeError(f"channel {self.name} is closed")

@@ -263,6 +263,23 @@ def test_argument_errors():
     assert not os.path.exists(f"/dev/shm/{nm}")                                  # the creator unlinked it
 
 
+def test_unlink_clears_a_name_left_behind():
+    nm = name()
+    first = KVChannel.create(nm, 4096, 2, 1)
+    with pytest.raises(_native.PaceKVError):
+        KVChannel.create(nm, 4096, 2, 1)
+    KVChannel.unlink(nm)                       # as after a creator that died
+    second = KVChannel.create(nm, 4096, 2, 1)  # a fresh channel under the same name
+    KVChannel.unlink(nm + "_never_created")    # not an error
+    first.close()                              # the name is second's now: first leaves it
+    assert os.path.exists(f"/dev/shm/{nm}")
+    third = KVChannel.open(nm, 1, timeout=5)   # and it still opens second's ring
+    assert third.slot_bytes == 4096
+    third.close()
+    second.close()
+    assert not os.path.exists(f"/dev/shm/{nm}")
+
+
 def test_kvref_round_trips_the_kvobj_fields():
     r = KVref(17, [5, 3, 9], 2.25, 1.0, 2.0, 0)
     h = MessageHeader(42, r.meta(), 32, 3, 65536)
