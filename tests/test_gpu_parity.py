@@ -274,6 +274,9 @@ def test_concurrent_host_threads_on_their_own_streams(gpu):
     sets = [(perm[t * share:(t + 1) * share].tolist(), perm.flip(0)[t * share:(t + 1) * share].tolist())
             for t in range(threads)]
     errors = []
+    # The pools were filled on the default stream, which the workers' streams
+    # (torch's pooled streams are non-blocking) do not wait for.
+    torch.cuda.synchronize()
 
     def worker(t):
         try:

@@ -100,6 +100,10 @@ def test_one_migrator_from_threads_on_their_own_streams(gpu):
     rng = np.random.default_rng(22)
     perm = rng.permutation(POOL).tolist()
     batches = [[perm[i * 40:(i + 1) * 40]] for i in range(8)]          # disjoint 40-page requests
+    # The pools were filled on the default stream, which the workers' streams
+    # (torch's pooled streams are non-blocking) do not wait for: without this,
+    # a destination fill still running could overwrite the first promotions.
+    torch.cuda.synchronize()
     for native in (False, True):
         alloc = (NativeBlockAllocator if native else BlockAllocator)(16, POOL)
         mig = migrate.KVMigrator(src, dst, alloc)
