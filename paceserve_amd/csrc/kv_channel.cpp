@@ -20,6 +20,12 @@
 // of host threads while chunk c+1 is packed and copied down; the receiver
 // copies a shared slot into a pinned slot (releasing the shared slot at once),
 // then uploads it and unpacks it while the next chunk is copied.
+//
+// Failures: every wait has a deadline and ends when either side closes the
+// channel; the control block records which process plays each role, so a
+// wait also ends when the peer process has exited.  A sender that fails
+// part-way marks its message abandoned; a receiver skips chunks left over
+// from a message it failed to take.
 #include <errno.h>
 #include <fcntl.h>
 #include <signal.h>
