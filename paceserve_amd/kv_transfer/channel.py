@@ -49,7 +49,12 @@ def _ms(timeout: float) -> int:
 
 
 class KVChannel:
-    """One endpoint of a channel (create() on one side, open() on the other)."""
+    """One endpoint of a channel (create() on one side, open() on the other).
+
+    Messages arrive in the order they were sent, and a message is received in
+    two calls (recv_header, then recv / recv_host / discard), so an endpoint
+    receives from one thread at a time; threads that each pull their own
+    sequences take a channel each."""
 
     def __init__(self, handle: int, name: str):
         self._handle = handle
