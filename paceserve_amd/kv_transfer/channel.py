@@ -17,8 +17,10 @@ pull model the decode side asks for a sequence and then receives it).
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import json
+import threading
 from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
@@ -52,9 +54,10 @@ class KVChannel:
     """One endpoint of a channel (create() on one side, open() on the other).
 
     Messages arrive in the order they were sent, and a message is received in
-    two calls (recv_header, then recv / recv_host / discard), so an endpoint
-    receives from one thread at a time; threads that each pull their own
-    sequences take a channel each."""
+    two calls (recv_header, then recv / recv_host / discard).  Threads that
+    share an endpoint take whole messages with message(), which holds the
+    endpoint's receive lock from the header to the end of the payload;
+    threads that each pull their own sequences take a channel each."""
 
     def __init__(self, handle: int, name: str):
         self._handle = handle
@@ -66,6 +69,7 @@ class KVChannel:
         self.num_slots = slots.value
         self._header: Optional[MessageHeader] = None
         self._inflight: list = []
+        self._rx_lock = threading.Lock()
 
     @classmethod
     def create(cls, name: str, slot_bytes: int = 32 * MiB, num_slots: int = 4,
@@ -149,6 +153,20 @@ class KVChannel:
             h = MessageHeader(msg.value, buf.raw[:meta_len.value], layers.value, n.value, pb.value)
             self._header = h if h.payload_bytes else None
             return h
+
+    @contextlib.contextmanager
+    def message(self, timeout: float = 60.0):
+        """Receives the next message's header under the endpoint's receive
+        lock and yields it; the body receives the payload (recv / recv_host),
+        and a payload left unreceived is drained on exit, so that several
+        threads can take whole messages from one endpoint."""
+        with self._rx_lock:
+            h = self.recv_header(timeout)
+            try:
+                yield h
+            finally:
+                if self._header is not None:
+                    self.discard(timeout)
 
     def recv(self, dst, page_ids: ops.IdsLike, timeout: float = 60.0,
              err: Optional[torch.Tensor] = None) -> None:

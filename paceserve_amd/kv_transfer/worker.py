@@ -20,6 +20,7 @@ bytes.
 """
 from __future__ import annotations
 
+import threading
 import time
 from dataclasses import dataclass
 from typing import Dict
@@ -62,6 +63,11 @@ class KVWorkerMixin:
     """Provides the worker's KV methods; the host class supplies
     `kvhelper` (a KVhelper), `seq_manager` and `local_rank`."""
 
+    # Inserting threads check for room and allocate as one step (the
+    # reference runs several insertion threads per instance,
+    # paceserve/disutil/decode_instance.py:50).
+    _alloc_lock = threading.Lock()
+
     def _get_kv_cache(self, seq):
         kv_cache, kv_indices = self.kvhelper.get_kv_cache(seq, self.seq_manager)
         self.seq_manager._free_seq(seq.seq_id)
@@ -76,11 +82,11 @@ class KVWorkerMixin:
         cached_content = kv_obj.kv_cache
         allocate_start = time.monotonic()
         bm = self.seq_manager.block_manager
-        if bm.get_num_free_gpu_blocks() >= bm.get_num_initial_blocks(seq):
+        with self._alloc_lock:
+            if bm.get_num_free_gpu_blocks() < bm.get_num_initial_blocks(seq):
+                return False
             self.seq_manager.add_seq(seq)
             bm.allocate(seq)
-        else:
-            return False
         kv_indices = self.seq_manager._get_block_table(seq)
         insert_start = time.monotonic()
         # A destination table one page longer than the source (the first
@@ -89,7 +95,6 @@ class KVWorkerMixin:
         status = self.kvhelper.insert_kv_cache(cached_content, ids, device)
         insert_time = time.monotonic() - insert_start
         return KVStatus(status, insert_time, insert_start - allocate_start)
-
 
     # ------------------------------------------------ cross-process channel
 
@@ -109,20 +114,40 @@ class KVWorkerMixin:
         sequence's."""
         from .channel import KVref
 
-        h = channel.recv_header(timeout)
-        ref = KVref.from_header(h)
-        if ref.seq_id != seq.seq_id:
-            channel.discard(timeout)
-            return False
+        with channel.message(timeout) as h:
+            ref = KVref.from_header(h)
+            if ref.seq_id != seq.seq_id:
+                return False
+            return self._insert_from_channel(seq, ref, channel, device, timeout)
+
+    def _recv_next_kv_cache(self, lookup, channel, device, timeout: float = 60.0):
+        """The next channel message, whichever sequence it carries, as the
+        reference's insertion threads insert whichever transfer finishes
+        first (paceserve/disutil/decode_instance.py:158-172): lookup(seq_id)
+        returns the sequence (None drains the message).  Several threads may
+        call this on one channel.  Returns (seq or seq_id, KVStatus or
+        False)."""
+        from .channel import KVref
+
+        with channel.message(timeout) as h:
+            ref = KVref.from_header(h)
+            seq = lookup(ref.seq_id)
+            if seq is None:
+                return ref.seq_id, False
+            return seq, self._insert_from_channel(seq, ref, channel, device, timeout)
+
+    def _insert_from_channel(self, seq, ref, channel, device, timeout: float):
+        """The allocation, remap and insert of _insert_kv_cache for a message
+        whose header was just received; returns KVStatus, or False (the
+        payload is then drained by the caller's message())."""
         block_len = len(ref.kv_indices)
         allocate_start = time.monotonic()
         bm = self.seq_manager.block_manager
-        if bm.get_num_free_gpu_blocks() >= bm.get_num_initial_blocks(seq):
+        with self._alloc_lock:
+            if bm.get_num_free_gpu_blocks() < bm.get_num_initial_blocks(seq):
+                return False
             self.seq_manager.add_seq(seq)
             bm.allocate(seq)
-        else:
-            channel.discard(timeout)
-            return False
         kv_indices = self.seq_manager._get_block_table(seq)
         insert_start = time.monotonic()
         ids = kv_indices if len(kv_indices) == block_len else kv_indices[:-1]

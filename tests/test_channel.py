@@ -280,6 +280,63 @@ def test_unlink_clears_a_name_left_behind():
     assert not os.path.exists(f"/dev/shm/{nm}")
 
 
+def test_threads_share_an_endpoint_message_by_message():
+    # Four receiving threads take whole messages from one endpoint with
+    # message(); every message arrives exactly once, whole.
+    tx, rx = pair(slot_bytes=4096, num_slots=3)
+    sent = {f"m{i}".encode(): payload(2, 3 + i, (2, 4, 1, 16), 50 + i) for i in range(12)}
+    got, errors = {}, []
+
+    def receive():
+        try:
+            while True:
+                with rx.message(timeout=10) as h:
+                    if h.meta == b"stop":
+                        return
+                    out = torch.empty((h.num_layers, h.n_pages, 2, 4, 1, 16), dtype=torch.float16)
+                    rx.recv_host(out, timeout=10)
+                    got[h.meta] = out
+        except Exception as e:                         # reported below
+            errors.append(repr(e))
+
+    ts = [threading.Thread(target=receive) for _ in range(4)]
+    for t in ts:
+        t.start()
+    for m, p in sent.items():
+        tx.send_host(p, m, timeout=10)
+    for _ in ts:
+        tx.send_host(torch.empty((0, 0, 2, 4, 1, 16), dtype=torch.float16), b"stop", timeout=10)
+    for t in ts:
+        t.join(timeout=30)
+    assert not errors, errors
+    assert sorted(got) == sorted(sent)
+    for m, p in sent.items():
+        assert torch.equal(got[m].view(torch.int16), p.view(torch.int16)), m
+    tx.close()
+    rx.close()
+
+
+def test_message_drains_a_payload_left_unreceived():
+    tx, rx = pair(slot_bytes=4096, num_slots=2)
+    a, b = payload(2, 20, (2, 4, 1, 16), 7), payload(1, 2, (2, 4, 1, 16), 8)
+
+    def send():
+        tx.send_host(a, b"a", timeout=10)
+        tx.send_host(b, b"b", timeout=10)
+
+    t = threading.Thread(target=send)
+    t.start()
+    with rx.message(timeout=10) as h:
+        assert h.meta == b"a"                          # payload not taken: drained on exit
+    with rx.message(timeout=10) as h:
+        out = torch.empty_like(b)
+        rx.recv_host(out, timeout=10)
+    t.join()
+    assert h.meta == b"b" and torch.equal(out.view(torch.int16), b.view(torch.int16))
+    tx.close()
+    rx.close()
+
+
 def test_kvref_round_trips_the_kvobj_fields():
     r = KVref(17, [5, 3, 9], 2.25, 1.0, 2.0, 0)
     h = MessageHeader(42, r.meta(), 32, 3, 65536)

@@ -2,7 +2,8 @@
 unpacked into another through the shared-memory ring, checked bit-exactly
 against torch's own gather; device and host payloads on either side; a
 sender in another process; and the worker methods that replace returning a
-KVobj through Ray (_send_kv_cache / _recv_kv_cache)."""
+KVobj through Ray (_send_kv_cache / _recv_kv_cache / _recv_next_kv_cache),
+with insertion threads sharing one channel."""
 import os
 import subprocess
 import sys
@@ -240,6 +241,65 @@ def test_worker_send_and_receive(gpu, tokens_src, tokens_dst):
                            words(src_cache[l][torch.tensor(src_table, device=gpu)]))
         untouched = sorted(set(range(POOL)) - set(dst_table[:n]))
         assert torch.equal(words(dst_cache[l][untouched]), before[l][untouched])
+
+
+def test_insertion_threads_share_one_channel(gpu):
+    """Four insertion threads take whichever sequence arrives next from one
+    channel (_recv_next_kv_cache), as the reference's insertion threads insert
+    whichever transfer finishes first; every sequence lands in its own
+    destination pages."""
+    src_w, src_cache = make_worker(gpu, 10)
+    dst_w, dst_cache = make_worker(gpu, 11)
+    lengths = [16 * k for k in (3, 1, 4, 2, 5, 2, 3, 1)]
+    seqs = [Sequence.of_length(f"s{i}", n, P) for i, n in enumerate(lengths)]
+    for s in seqs:
+        src_w.seq_manager.add_seq(s)
+        src_w.seq_manager.block_manager.allocate(s)
+    src_tables = {s.seq_id: src_w.seq_manager._get_block_table(s) for s in seqs}
+    want = {s.seq_id: [c[torch.tensor(src_tables[s.seq_id], device=gpu)].clone() for c in src_cache] for s in seqs}
+    torch.cuda.synchronize()
+    dst_seqs = {s.seq_id: Sequence.of_length(s.seq_id, n, P) for s, n in zip(seqs, lengths)}
+    results, errors = {}, []
+    lock = threading.Lock()
+
+    def insertion_thread(rx):
+        # takes messages until it takes a stop message (the sender sends one
+        # per thread after the sequences)
+        try:
+            while True:
+                seq, status = dst_w._recv_next_kv_cache(dst_seqs.get, rx, gpu, timeout=30)
+                if isinstance(seq, str) and seq.startswith("stop"):
+                    return
+                with lock:
+                    results[seq.seq_id] = status
+        except Exception as e:                         # reported below
+            errors.append(repr(e))
+
+    def recv(rx):
+        ts = [threading.Thread(target=insertion_thread, args=(rx,)) for _ in range(4)]
+        for t in ts:
+            t.start()
+        for t in ts:
+            t.join(timeout=60)
+        torch.cuda.synchronize()
+
+    def send(tx):
+        for s in seqs:
+            src_w._send_kv_cache(s, tx)
+        # one empty message per thread still waiting, so that every thread returns
+        for i in range(4):
+            tx.send_host(torch.empty((0, 0, 2, P, H, D), dtype=torch.float16),
+                         KVref(f"stop{i}", [], 0.0).meta(), timeout=30)
+
+    run_pair(1 << 20, 3, send, recv)
+    assert not errors, errors
+    for s in seqs:
+        st = results[s.seq_id]
+        assert isinstance(st, KVStatus) and st.status, s.seq_id
+        table = dst_w.seq_manager._get_block_table(dst_seqs[s.seq_id])
+        for l in range(L):
+            assert torch.equal(words(dst_cache[l][torch.tensor(table, device=gpu)]), words(want[s.seq_id][l])), \
+                f"{s.seq_id} layer {l}"
 
 
 def test_worker_receive_refusals_drain_the_message(gpu):
