@@ -1,8 +1,8 @@
 """The cross-process channel's protocol on host payloads (no GPU): messages in
 order with their metadata, payloads larger than the ring streaming through
 it, layer- and page-sized chunks, another process as the sender, deadlines,
-closing, abandoned messages, draining, a peer process that dies mid-message,
-and argument errors."""
+closing, abandoned messages, draining, threads sharing an endpoint message by
+message, a peer process that dies mid-message, and argument errors."""
 import os
 import subprocess
 import sys
