@@ -15,7 +15,6 @@ import pytest
 import torch
 
 from paceserve_amd.core.sequence import Sequence
-from paceserve_amd.kv_transfer import ops
 from paceserve_amd.kv_transfer.channel import KVChannel, KVref
 from paceserve_amd.kv_transfer.kv_utils import KVhelper
 from paceserve_amd.kv_transfer.worker import KVStatus, KVWorker, WorkerSequenceManager

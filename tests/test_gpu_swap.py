@@ -1,7 +1,6 @@
 """Swap-out / swap-in between a device pool and a pinned host page pool
 (pace_kv_swap_out / pace_kv_swap_in), the host-pointer checks that keep the
 kernel off unregistered memory, and SwapSpace for preempted requests."""
-import ctypes
 
 import numpy as np
 import pytest
