@@ -334,11 +334,13 @@ int resolve_layers(const void* const* layers, int num_layers, int64_t pool_bytes
     if (!host && attr.device != dev)
       return fail(PACE_KV_EINVAL, "%s: layer %d lives on device %d, current device is %d", what, l,
                   attr.device, dev);
+    // The allocation's range comes from hipMemGetAddressRange: on ROCm 7.2,
+    // hipPointerGetAttribute(HIP_POINTER_ATTRIBUTE_RANGE_SIZE) reports the
+    // size modulo 2^32 (a 4 GiB allocation reads 0), which would reject a
+    // valid pool carved out of a large allocation or accept a short one.
     hipDeviceptr_t start = nullptr;
     size_t size = 0;
-    e = hipPointerGetAttribute(&start, HIP_POINTER_ATTRIBUTE_RANGE_START_ADDR, const_cast<void*>(p));
-    if (e == hipSuccess)
-      e = hipPointerGetAttribute(&size, HIP_POINTER_ATTRIBUTE_RANGE_SIZE, const_cast<void*>(p));
+    e = hipMemGetAddressRange(&start, &size, const_cast<void*>(p));
     if (e != hipSuccess) {
       (void)hipGetLastError();
       return fail(PACE_KV_EINVAL, "%s: layer %d allocation range unknown", what, l);

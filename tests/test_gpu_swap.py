@@ -79,6 +79,46 @@ def test_swap_rejects_pageable_and_short_host_memory(gpu):
         ops.PagedPool(pageable, host=True)
 
 
+def test_swap_pool_inside_a_4gib_allocation(gpu):
+    """Layers carved out of one device allocation of exactly 4 GiB, the last
+    one ending at the allocation's end: the pointer check must see the whole
+    allocation (hipPointerGetAttribute's RANGE_SIZE reads such a size modulo
+    2^32, i.e. 0), and must still refuse a pool that runs one page past it."""
+    torch.cuda.empty_cache()
+    big = torch.empty(1 << 32, dtype=torch.uint8, device=gpu)
+    pages, pb = 64, SHAPE.page_bytes
+    lb = pages * pb
+    offsets = [0, lb, 2 * lb, (1 << 32) - 2 * lb, (1 << 32) - lb]
+    g = torch.Generator(device=gpu).manual_seed(11)
+    layers = []
+    for off in offsets:
+        t = big[off:off + lb].view(SHAPE.dtype).view((pages,) + SHAPE.page_shape)
+        t.copy_(torch.randn(t.shape, generator=g, device=gpu, dtype=torch.float32))
+        layers.append(t)
+    dev = ops.PagedPool(layers)
+    host = ops.HostPagePool.like(dev, 8)
+    d_ids, h_ids = [63, 0, 17, 40], [5, 1, 7, 0]
+    ops.swap_out(dev, d_ids, host, h_ids)
+    torch.cuda.synchronize()
+    for l in range(SHAPE.num_layers):
+        want = layers[l][torch.tensor(d_ids, device=gpu)].cpu()
+        assert torch.equal(words(host.layers[l][h_ids]), words(want))
+    back_ids = [2, 3, 62, 61]
+    ops.swap_in(host, h_ids, dev, back_ids)
+    torch.cuda.synchronize()
+    for l in range(SHAPE.num_layers):
+        assert torch.equal(words(layers[l][torch.tensor(back_ids, device=gpu)]),
+                           words(layers[l][torch.tensor(d_ids, device=gpu)]))
+    ids = torch.arange(2, dtype=torch.int32, device=gpu)
+    rc = _native.load().pace_kv_swap_out(
+        dev.table(), pages + 1, ids.data_ptr(), host.table(), 8, ids.data_ptr(),
+        dev.num_layers, 2, pb, None, torch.cuda.current_stream().cuda_stream)
+    assert rc == _native.PACE_KV_ERANGE
+    assert "layer 4 allocation holds" in _native.load().pace_kv_last_error().decode()
+    del layers, dev, big
+    torch.cuda.empty_cache()
+
+
 def test_swap_space_preemption_round_trip(gpu):
     dev = dev_pool(gpu, 128, 5)
     alloc = NativeBlockAllocator(16, 128)
