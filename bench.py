@@ -208,7 +208,7 @@ def run_device(args, w, dev, src, dst, plan, s_ids, d_ids):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": copy_kernel_names(args.mode, min(k, L) * n * w.shape.page_bytes, w.shape.page_bytes),
+            "kernel": copy_kernel_names(args.mode, w.shape.page_bytes),
             "algorithmic_bytes_per_launch": int(statistics.mean(bytes_per_launch)),
             "mean_launch_us": round(mean_launch_ms * 1e3, 2),
             "launch_timing": "HIP events around the K timed steps on the launch stream, divided by "
@@ -220,27 +220,21 @@ def run_device(args, w, dev, src, dst, plan, s_ids, d_ids):
     return res
 
 
-# Pack launches writing at most this many bytes use plain stores (the
-# library's kTemporalStoreMaxBytes); every other copy uses nontemporal stores.
-TEMPORAL_STORE_MAX_BYTES = 1 << 30
-
-
-def copy_kernel_names(mode: str, launch_payload: int, page_bytes: int) -> str:
+def copy_kernel_names(mode: str, page_bytes: int) -> str:
     """The page_copy_kernel instances a step launches (template arguments
-    GUARD = page not a multiple of 1 KiB rows, TEMPORAL = plain stores,
-    POW2 = a power-of-two number of rows per page)."""
+    GUARD = page not a multiple of 1 KiB rows, PACK = the pack's cacheable
+    write-through stores rather than streaming ones, POW2 = a power-of-two
+    number of rows per page)."""
     guard = "true" if page_bytes % 1024 else "false"
     rows = -(-page_bytes // 1024)
     pow2 = "true" if rows & (rows - 1) == 0 else "false"
 
-    def k(temporal: str) -> str:
-        return f"page_copy_kernel<{guard}, {temporal}, {pow2}>"
+    def k(pack: str) -> str:
+        return f"page_copy_kernel<{guard}, {pack}, {pow2}>"
 
     if mode == "fused":
-        return f"{k('false')} (move, nontemporal stores)"
-    if launch_payload <= TEMPORAL_STORE_MAX_BYTES:
-        return f"{k('true')} (pack, plain stores) and {k('false')} (unpack, nontemporal stores)"
-    return f"{k('false')} (pack and unpack, nontemporal stores)"
+        return f"{k('false')} (move, streaming write-through stores)"
+    return f"{k('true')} (pack, write-through stores) and {k('false')} (unpack, streaming write-through stores)"
 
 
 def run_ceiling(w, dev, src, dst, n: int, reps: int = 10) -> dict:

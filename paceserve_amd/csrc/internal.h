@@ -35,15 +35,17 @@ struct Side {
 // Most page ids per side that a launch carries in its kernel arguments.
 #define PACE_KV_INLINE_IDS 512
 
+// Store flavour of a copy: both write through the L2 at device scope; kStream
+// also marks the stores nontemporal, while kPack (a pack into a transfer
+// buffer) leaves them cacheable, so that the unpack reading the rows next
+// finds them in the memory-side cache.
+enum class StorePolicy { kStream, kPack };
+
 // Validates arguments and enqueues the copy dst[l][dst_id(j)] = src[l][src_id(j)]
 // for l < num_layers, j < n_pages on `stream`, in launches of at most
 // PACE_KV_MAX_LAYERS_PER_LAUNCH layers.  host_src_ids / host_dst_ids (host
 // arrays, n_pages <= PACE_KV_INLINE_IDS) replace the sides' device ids and
 // travel in the kernel arguments.
-// Store flavour of a copy: kStream always uses nontemporal stores;
-// kTemporalIfSmall (pack) uses plain stores when one launch writes at most
-// 1 GiB, so that the unpack reading the rows next finds them in cache.
-enum class StorePolicy { kStream, kTemporalIfSmall };
 
 int launch_page_copy(const Side& src, const Side& dst, int num_layers,
                      int64_t n_pages, int64_t page_bytes, int32_t* err_count,

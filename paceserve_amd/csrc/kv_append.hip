@@ -79,6 +79,9 @@ __global__ __launch_bounds__(kThreads) void append_kernel(const AppendParams p) 
   char* dst = p.cache + static_cast<int64_t>(page) * page_bytes +
               (static_cast<int64_t>(kv) * p.page_size + slot) * p.row_bytes;
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + vec);
+  // A plain nontemporal store: unlike the page copy, the append measured
+  // slower with the device-scope write-through store (prefill 16 x 1024
+  // tokens 25.3 us against 23.9-24.7 us per launch, decode 2.37 against 2.22).
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst) + vec);
 }
 

@@ -12,7 +12,7 @@
 // Work decomposition.  A page of one layer is `page_bytes` contiguous bytes
 // (K half then V half).  It is split into 1 KiB rows; one workgroup of one
 // wave64 copies one row, each lane moving one 16-byte vector with a
-// nontemporal load and a nontemporal store, and then retires.  The grid is
+// nontemporal load and a write-through store, and then retires.  The grid is
 // (rows x pages) x layers: blockIdx.x walks the rows of a layer's pages, row
 // fastest, and blockIdx.y is the layer, so workgroups dispatched together read
 // (unpack) or write (pack) adjacent rows of the transfer buffer and adjacent
@@ -40,14 +40,6 @@ constexpr int kThreads = 64;              // one wave64 per workgroup
 constexpr int kVecBytes = 16;
 constexpr int kRowBytes = kThreads * kVecBytes;  // 1 KiB per workgroup
 constexpr int kMaxLayers = PACE_KV_MAX_LAYERS_PER_LAUNCH;
-// Pack launches that write at most this many bytes use plain stores: measured
-// on MI355X, the packed rows then stay in the caches for the unpack that reads
-// them next (pack+unpack +5..9% for 64 MiB-512 MiB per launch, +1.5% at
-// 1 GiB), while larger launches are faster with nontemporal stores (-1.7% at
-// 2 GiB, -2.6% at 4 GiB).  Unpack, move and swaps, whose output nothing reads
-// back soon, keep nontemporal stores (a fused move of 512 MiB with plain
-// stores ends ~6% later, the dirty lines draining before completion).
-constexpr int64_t kTemporalStoreMaxBytes = int64_t(1) << 30;
 // Workgroups per launch stay below 2^25 so that grid * 64 threads fits the
 // 32-bit launch limit with room to spare; larger batches use more launches.
 constexpr int64_t kMaxItemsPerLaunch = int64_t(1) << 25;
@@ -82,19 +74,26 @@ __device__ __forceinline__ uint32_t page_of(const int32_t* ids, uint32_t j) {
   return ids ? static_cast<uint32_t>(ids[j]) : j;
 }
 
-template <bool TEMPORAL>
+// Stores carry the device-scope bit (sc1): an XCD's L2 is not coherent with
+// the other XCDs', so such a store writes through it to the memory side, and
+// the launch leaves no dirty L2 lines to write back when it ends.  A pack
+// (PACK) stores with sc1 alone, so the rows also stay in the memory-side cache
+// for the unpack that reads them next; every other copy adds nt (streaming).
+// Measured on MI355X against plain (launches <= 1 GiB) or nontemporal pack
+// stores and nontemporal unpack stores, pack+unpack runs 0.8% (16 GiB of
+// 256 KiB pages) to 5.9% (64 MiB) faster, and a fused move 0.5% to 4.2%.
+template <bool PACK>
 __device__ __forceinline__ void store_vec(const u32x4 v, u32x4* d) {
-  if (TEMPORAL) *d = v;
-  else __builtin_nontemporal_store(v, d);
+  if (PACK) asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(d), "v"(v) : "memory");
+  else asm volatile("global_store_dwordx4 %0, %1, off nt sc1" : : "v"(d), "v"(v) : "memory");
 }
 
 // The copy of one 1 KiB row: item blockIdx.x (page j, row r of it) of layer
 // blockIdx.y; the grid is exactly (rows x pages) x layers.  POW2: the page has
 // a power-of-two number of rows.  sids / dids are the sides' page ids (device
 // or kernel-argument arrays), nullptr for a contiguous side.  Loads are
-// always nontemporal; TEMPORAL selects plain stores (kept in the memory-side
-// cache) instead of nontemporal ones.
-template <bool GUARD, bool TEMPORAL, bool POW2>
+// always nontemporal; PACK selects the pack's store policy (store_vec).
+template <bool GUARD, bool PACK, bool POW2>
 __device__ __forceinline__ void copy_row(const CopyParams& p, const int32_t* sids,
                                          const int32_t* dids) {
   const uint32_t x = blockIdx.x;
@@ -114,7 +113,7 @@ __device__ __forceinline__ void copy_row(const CopyParams& p, const int32_t* sid
       if (row == 0 && threadIdx.x == 0 && p.err != nullptr) atomicAdd(p.err, 1);
       return;
     }
-    store_vec<TEMPORAL>(v, reinterpret_cast<u32x4*>(p.dst[layer] + static_cast<int64_t>(dp) * p.page_bytes) + vec);
+    store_vec<PACK>(v, reinterpret_cast<u32x4*>(p.dst[layer] + static_cast<int64_t>(dp) * p.page_bytes) + vec);
     return;
   }
   const uint32_t sp = static_cast<uint32_t>(sids[j]);
@@ -126,29 +125,29 @@ __device__ __forceinline__ void copy_row(const CopyParams& p, const int32_t* sid
   }
   const u32x4 v = __builtin_nontemporal_load(
       reinterpret_cast<const u32x4*>(p.src[layer] + static_cast<int64_t>(sp) * p.page_bytes) + vec);
-  store_vec<TEMPORAL>(v, reinterpret_cast<u32x4*>(p.dst[layer] + static_cast<int64_t>(dp) * p.page_bytes) + vec);
+  store_vec<PACK>(v, reinterpret_cast<u32x4*>(p.dst[layer] + static_cast<int64_t>(dp) * p.page_bytes) + vec);
 }
 
 // GUARD: page_bytes is not a multiple of kRowBytes, so the last row of a page
 // is partial.
-template <bool GUARD, bool TEMPORAL, bool POW2>
+template <bool GUARD, bool PACK, bool POW2>
 __global__ __launch_bounds__(kThreads) void page_copy_kernel(const CopyParams p) {
-  copy_row<GUARD, TEMPORAL, POW2>(p, p.src_ids, p.dst_ids);
+  copy_row<GUARD, PACK, POW2>(p, p.src_ids, p.dst_ids);
 }
 
 // Same copy with the ids in the kernel arguments.  A side whose ids are not
 // inline (the contiguous buffer of a pack or unpack) indexes pages by
 // position.
-template <bool GUARD, bool TEMPORAL, bool POW2, bool SRC_INLINE, bool DST_INLINE>
+template <bool GUARD, bool PACK, bool POW2, bool SRC_INLINE, bool DST_INLINE>
 __global__ __launch_bounds__(kThreads) void page_copy_inline_kernel(const CopyParamsInline p) {
-  copy_row<GUARD, TEMPORAL, POW2>(p.base, SRC_INLINE ? p.src_ids : nullptr,
-                                  DST_INLINE ? p.dst_ids : nullptr);
+  copy_row<GUARD, PACK, POW2>(p.base, SRC_INLINE ? p.src_ids : nullptr,
+                              DST_INLINE ? p.dst_ids : nullptr);
 }
 
-template <bool GUARD, bool TEMPORAL, bool POW2>
+template <bool GUARD, bool PACK, bool POW2>
 hipError_t launch_t(const CopyParams& p, dim3 grid, hipStream_t stream) {
   void* args[] = {const_cast<CopyParams*>(&p)};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&page_copy_kernel<GUARD, TEMPORAL, POW2>), grid,
+  return hipLaunchKernel(reinterpret_cast<const void*>(&page_copy_kernel<GUARD, PACK, POW2>), grid,
                          dim3(kThreads), args, 0, stream);
 }
 
@@ -156,36 +155,36 @@ hipError_t launch_t(const CopyParams& p, dim3 grid, hipStream_t stream) {
 // only (unpack).
 enum InlineSides { kBothInline = 0, kSrcInline = 1, kDstInline = 2 };
 
-template <bool GUARD, bool TEMPORAL, bool POW2, int SIDES>
+template <bool GUARD, bool PACK, bool POW2, int SIDES>
 hipError_t launch_inline_t(const CopyParamsInline& p, dim3 grid, hipStream_t stream) {
   void* args[] = {const_cast<CopyParamsInline*>(&p)};
   constexpr bool kS = SIDES != kDstInline, kD = SIDES != kSrcInline;
   return hipLaunchKernel(
-      reinterpret_cast<const void*>(&page_copy_inline_kernel<GUARD, TEMPORAL, POW2, kS, kD>), grid,
+      reinterpret_cast<const void*>(&page_copy_inline_kernel<GUARD, PACK, POW2, kS, kD>), grid,
       dim3(kThreads), args, 0, stream);
 }
 
 using LaunchFn = hipError_t (*)(const CopyParams&, dim3, hipStream_t);
 using LaunchInlineFn = hipError_t (*)(const CopyParamsInline&, dim3, hipStream_t);
 
-// Instances indexed [GUARD][TEMPORAL][POW2] (and [SIDES] for inline ids).
+// Instances indexed [GUARD][PACK][POW2] (and [SIDES] for inline ids).
 constexpr LaunchFn kLaunch[2][2][2] = {
     {{launch_t<false, false, false>, launch_t<false, false, true>},
      {launch_t<false, true, false>, launch_t<false, true, true>}},
     {{launch_t<true, false, false>, launch_t<true, false, true>},
      {launch_t<true, true, false>, launch_t<true, true, true>}}};
 
-template <bool GUARD, bool TEMPORAL, bool POW2>
-constexpr LaunchInlineFn kInlineSides[3] = {launch_inline_t<GUARD, TEMPORAL, POW2, kBothInline>,
-                                            launch_inline_t<GUARD, TEMPORAL, POW2, kSrcInline>,
-                                            launch_inline_t<GUARD, TEMPORAL, POW2, kDstInline>};
+template <bool GUARD, bool PACK, bool POW2>
+constexpr LaunchInlineFn kInlineSides[3] = {launch_inline_t<GUARD, PACK, POW2, kBothInline>,
+                                            launch_inline_t<GUARD, PACK, POW2, kSrcInline>,
+                                            launch_inline_t<GUARD, PACK, POW2, kDstInline>};
 
-LaunchInlineFn launch_inline_fn(bool guard, bool temporal, bool pow2, int sides) {
+LaunchInlineFn launch_inline_fn(bool guard, bool pack, bool pow2, int sides) {
   if (guard) {
-    if (temporal) return pow2 ? kInlineSides<true, true, true>[sides] : kInlineSides<true, true, false>[sides];
+    if (pack) return pow2 ? kInlineSides<true, true, true>[sides] : kInlineSides<true, true, false>[sides];
     return pow2 ? kInlineSides<true, false, true>[sides] : kInlineSides<true, false, false>[sides];
   }
-  if (temporal) return pow2 ? kInlineSides<false, true, true>[sides] : kInlineSides<false, true, false>[sides];
+  if (pack) return pow2 ? kInlineSides<false, true, true>[sides] : kInlineSides<false, true, false>[sides];
   return pow2 ? kInlineSides<false, false, true>[sides] : kInlineSides<false, false, false>[sides];
 }
 
@@ -291,17 +290,16 @@ int launch_page_copy(const Side& src, const Side& dst, int num_layers, int64_t n
       p.rows_per_page = static_cast<uint32_t>(rows_per_page);
       p.rows_log2 = rows_log2;
       const dim3 grid(static_cast<uint32_t>(rows_per_page * nj), static_cast<uint32_t>(nl));
-      const bool temporal = policy == StorePolicy::kTemporalIfSmall &&
-                            int64_t(nl) * nj * page_bytes <= kTemporalStoreMaxBytes;
+      const bool pack = policy == StorePolicy::kPack;
       if (inline_ids) {
         CopyParamsInline q;
         q.base = p;
         if (host_src_ids) memcpy(q.src_ids, host_src_ids + j0, nj * sizeof(int32_t));
         if (host_dst_ids) memcpy(q.dst_ids, host_dst_ids + j0, nj * sizeof(int32_t));
         const int sides = host_src_ids && host_dst_ids ? kBothInline : (host_src_ids ? kSrcInline : kDstInline);
-        rc = hip_status(launch_inline_fn(guard, temporal, pow2, sides)(q, grid, stream), "page copy launch");
+        rc = hip_status(launch_inline_fn(guard, pack, pow2, sides)(q, grid, stream), "page copy launch");
       } else {
-        rc = hip_status(kLaunch[guard][temporal][pow2](p, grid, stream), "page copy launch");
+        rc = hip_status(kLaunch[guard][pack][pow2](p, grid, stream), "page copy launch");
       }
       if (rc) return rc;
     }
@@ -404,7 +402,7 @@ int pace_kv_pack(const void* const* src_layers, int num_layers, int64_t pool_pag
   Side dst{buf.data(), nullptr, n_pages};
   return pace_kv::launch_page_copy(src, dst, num_layers, n_pages, page_bytes, err_count,
                                    static_cast<hipStream_t>(stream), nullptr, nullptr,
-                                   pace_kv::StorePolicy::kTemporalIfSmall);
+                                   pace_kv::StorePolicy::kPack);
 }
 
 int pace_kv_unpack(const void* buf, int64_t buf_layer_stride, void* const* dst_layers,

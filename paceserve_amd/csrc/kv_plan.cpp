@@ -179,7 +179,7 @@ int promote_inline(pace_kv_promoter* pr, pace_kv_allocator* dst_alloc,
         rc = pace_kv::launch_page_copy(Side{src_tab + l0, nullptr, src_pool_pages},
                                        Side{buf.data(), nullptr, n}, nl, n, page_bytes, err_count,
                                        stream, src_ids, nullptr,
-                                       pace_kv::StorePolicy::kTemporalIfSmall);
+                                       pace_kv::StorePolicy::kPack);
         if (rc == PACE_KV_OK)
           rc = pace_kv::launch_page_copy(Side{buf.data(), nullptr, n},
                                          Side{dst_tab + l0, nullptr, dst_pool_pages}, nl, n,

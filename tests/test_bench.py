@@ -25,15 +25,12 @@ def write_csv(path, rows):
 
 
 def test_copy_kernel_names_follow_the_store_policy():
-    big = bench.TEMPORAL_STORE_MAX_BYTES + 1
-    assert bench.copy_kernel_names("buffer", big, 65536) == \
-        "page_copy_kernel<false, false, true> (pack and unpack, nontemporal stores)"
-    small = bench.copy_kernel_names("buffer", 64 << 20, 65536)
-    assert "page_copy_kernel<false, true, true> (pack, plain stores)" in small
-    assert "page_copy_kernel<false, false, true> (unpack" in small
+    names = bench.copy_kernel_names("buffer", 65536)
+    assert "page_copy_kernel<false, true, true> (pack, write-through stores)" in names
+    assert "page_copy_kernel<false, false, true> (unpack" in names
     # 96 B: one partial row (a power of two); 3 KiB: three rows (not)
-    assert bench.copy_kernel_names("fused", 64 << 20, 96).startswith("page_copy_kernel<true, false, true> (move")
-    assert bench.copy_kernel_names("fused", 64 << 20, 3072).startswith("page_copy_kernel<false, false, false>")
+    assert bench.copy_kernel_names("fused", 96).startswith("page_copy_kernel<true, false, true> (move")
+    assert bench.copy_kernel_names("fused", 3072).startswith("page_copy_kernel<false, false, false>")
 
 
 def test_summarize_pmc_scales_counters_by_the_calibration_copy(tmp_path):
