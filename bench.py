@@ -804,6 +804,9 @@ def run_calibration(dev) -> None:
     log(f"calibration: {CALIBRATION_COPIES} x 1 GiB torch copy_ done")
 
 
+CPU_SAMPLE_SECONDS = 10.0
+
+
 def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan):
     """The reference's CPU path on pageable host tensors: per layer,
     index_select into the buffer then index_copy_ into the destination.  The
@@ -821,12 +824,12 @@ def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan):
     s_idx = torch.tensor(plan.src_ids, dtype=torch.long)
     d_idx = torch.tensor(plan.dst_ids, dtype=torch.long)
     buf = torch.empty((L, plan.n_pages) + w.shape.page_shape, dtype=w.shape.dtype)
-    t0 = time.perf_counter()
-    orc.torch_cpu_pack_unpack(src, s_idx, dst, d_idx, buf)            # warm-up
-    first = time.perf_counter() - t0
-    reps = int(min(50, max(5, 10.0 // max(first, 1e-3))))            # ~10 s of CPU work
+    for _ in range(2):                                                # warm-up (first touch)
+        orc.torch_cpu_pack_unpack(src, s_idx, dst, d_idx, buf)
+    # Passes until CPU_SAMPLE_SECONDS of work are timed (5 to 5000 passes).
     times = []
-    for _ in range(reps):
+    end = time.perf_counter() + CPU_SAMPLE_SECONDS
+    while len(times) < 5 or (len(times) < 5000 and time.perf_counter() < end):
         t0 = time.perf_counter()
         orc.torch_cpu_pack_unpack(src, s_idx, dst, d_idx, buf)
         times.append(time.perf_counter() - t0)
@@ -838,8 +841,9 @@ def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan):
         "cores": cores,
         "kind": "port",
         "sample": f"{L} of {w.shape.num_layers} layers, all {plan.n_pages} pages of {w.name} "
-                  f"({payload / 2**30:.2f} GiB payload), full-size pools per layer; median of {reps} "
-                  f"after 1 warm-up; torch {torch.__version__} index_select/index_copy_ on host tensors",
+                  f"({payload / 2**30:.2f} GiB payload), full-size pools per layer; median of {len(times)} "
+                  f"passes ({sum(times):.1f} s) after 2 warm-up passes; torch {torch.__version__} "
+                  f"index_select/index_copy_ on host tensors",
         "seconds_per_pass": round(t, 4),
     }
 
@@ -857,7 +861,7 @@ def _rows(csv_path: str) -> list:
 def _json(path: str) -> dict:
     with open(path) as f:
         return json.load(f)
-KERNEL_TAG = "page_copy_kernel<false, false, true>"
+KERNEL_TAG = "page_copy_kernel"
 
 
 # Copies of 1 GiB that --calibrate runs last in a bench run.
