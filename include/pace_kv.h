@@ -376,7 +376,8 @@ int pace_kv_promote(pace_kv_promoter* promoter, pace_kv_allocator* dst_alloc,
 typedef struct pace_kv_channel pace_kv_channel;
 
 /* Creates the channel "/<name>" (fails with PACE_KV_ESTATE if it exists):
- * num_slots in [2, 64] slots of slot_bytes (a multiple of 4096).  The
+ * num_slots (a power of two in [2, 64]) slots of slot_bytes (a multiple of
+ * 4096).  The
  * creator's close unlinks the name.  copy_threads in [1, 64]. */
 int pace_kv_channel_create(const char* name, int64_t slot_bytes, int num_slots,
                            int copy_threads, pace_kv_channel** out);

@@ -7,7 +7,9 @@
 //   num_slots data slots of slot_bytes each, page-aligned
 // One sender and one receiver (single producer, single consumer).  The sender
 // owns `head` (slots published), the receiver owns `tail` (slots released);
-// both are 32-bit futex words, compared modulo 2^32.  A slot holds one record:
+// both are 32-bit futex words, compared modulo 2^32, and the slot count is a
+// power of two so that the slot of a record stays the count modulo num_slots
+// across the wrap.  A slot holds one record:
 // a message header (shape + an opaque metadata blob) or one chunk of the
 // message's payload.  The payload is the contiguous transfer-buffer layout
 // [num_layers][n_pages][page_bytes]; a chunk is a run of whole layers when a
@@ -27,6 +29,7 @@
 // part-way marks its message abandoned; a receiver skips chunks left over
 // from a message it failed to take.
 #include <errno.h>
+#include <stddef.h>
 #include <fcntl.h>
 #include <signal.h>
 #include <stdio.h>
@@ -100,6 +103,14 @@ struct alignas(64) ChannelCtl {
   ProcessId sender, receiver;
   SlotRecord slots[kMaxSlots];
 };
+
+// head and tail count records modulo 2^32 and a record's slot is the count
+// modulo num_slots; a power-of-two slot count divides 2^32, so consecutive
+// records keep consecutive slots across the counters' wrap.
+static_assert(offsetof(ChannelCtl, head) == 64 && offsetof(ChannelCtl, tail) == 128,
+              "control-block layout (the wrap test sets head and tail at these offsets)");
+
+bool valid_slot_count(int64_t n) { return n >= 2 && n <= kMaxSlots && (n & (n - 1)) == 0; }
 
 int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
@@ -624,9 +635,10 @@ int pace_kv_channel_create(const char* name, int64_t slot_bytes, int num_slots, 
     delete ch;
     return fail(PACE_KV_EINVAL, "channel: slot_bytes must be a positive multiple of 4096");
   }
-  if (num_slots < 2 || num_slots > kMaxSlots) {
+  if (!valid_slot_count(num_slots)) {
     delete ch;
-    return fail(PACE_KV_EINVAL, "channel: num_slots must be in [2, %d]", kMaxSlots);
+    return fail(PACE_KV_EINVAL, "channel: num_slots must be a power of two in [2, %d] (got %d)", kMaxSlots,
+                num_slots);
   }
   if (slot_bytes > (INT64_MAX / 2) / num_slots) {
     delete ch;
@@ -704,8 +716,8 @@ int pace_kv_channel_open(const char* name, int copy_threads, int timeout_ms, pac
     std::this_thread::sleep_for(std::chrono::milliseconds(1));
   }
   ChannelCtl* c = ch->ctl;
-  if (c->version != kVersion || c->total_bytes != ch->map_bytes || c->num_slots < 2 ||
-      c->num_slots > kMaxSlots) {
+  if (c->version != kVersion || c->total_bytes != ch->map_bytes ||
+      !valid_slot_count(static_cast<int64_t>(c->num_slots))) {
     destroy(ch);
     return fail(PACE_KV_ESTATE, "channel %s: incompatible control block", name);
   }

@@ -74,6 +74,8 @@ class KVChannel:
     @classmethod
     def create(cls, name: str, slot_bytes: int = 32 * MiB, num_slots: int = 4,
                copy_threads: int = 4) -> "KVChannel":
+        """Creates the ring (num_slots: a power of two in [2, 64]; slot_bytes:
+        a multiple of 4096) and returns the creating endpoint."""
         handle = ctypes.c_void_p()
         _native.check(_native.load().pace_kv_channel_create(name.encode(), int(slot_bytes), int(num_slots),
                                                             int(copy_threads), ctypes.byref(handle)))

@@ -35,7 +35,7 @@ def payload(L, n, page_shape, seed, dtype=torch.float16):
     return torch.randn((L, n) + tuple(page_shape), generator=g).to(dtype)
 
 
-def pair(slot_bytes=64 << 10, num_slots=3, threads=4):
+def pair(slot_bytes=64 << 10, num_slots=4, threads=4):
     nm = name()
     rx = KVChannel.create(nm, slot_bytes, num_slots, threads)
     tx = KVChannel.open(nm, threads, timeout=5)
@@ -104,7 +104,7 @@ ch.close()
 
 def test_another_process_sends():
     nm = name()
-    rx = KVChannel.create(nm, 8192, 3, 4)
+    rx = KVChannel.create(nm, 8192, 4, 4)
     child = subprocess.Popen([sys.executable, "-c", SENDER.format(root=str(ROOT), name=nm)])
     try:
         for i in range(5):
@@ -232,7 +232,7 @@ def test_argument_errors():
     for bad_name in (b"", b"a/b", b"x" * 300):
         assert lib.pace_kv_channel_create(bad_name, 4096, 2, 1, __import__("ctypes").byref(h)) == _native.PACE_KV_EINVAL
     nm = name()
-    for slot, slots, thr in ((100, 2, 1), (4096, 1, 1), (4096, 65, 1), (4096, 2, 0)):
+    for slot, slots, thr in ((100, 2, 1), (4096, 1, 1), (4096, 3, 1), (4096, 48, 1), (4096, 128, 1), (4096, 2, 0)):
         with pytest.raises(_native.PaceKVError) as e:
             KVChannel.create(nm, slot, slots, thr)
         assert status(e) == _native.PACE_KV_EINVAL
@@ -280,10 +280,41 @@ def test_unlink_clears_a_name_left_behind():
     assert not os.path.exists(f"/dev/shm/{nm}")
 
 
+def test_record_counters_wrap_at_2_32():
+    # The control block counts records in two 32-bit words (head at byte 64,
+    # tail at byte 128, pinned by a static_assert in the library).  Starting
+    # both just below 2^32, a stream of multi-chunk messages crosses the wrap
+    # with every payload intact and in order.
+    import mmap
+    import struct
+
+    tx, rx = pair(slot_bytes=4096, num_slots=4)
+    start = (1 << 32) - 6
+    with open(f"/dev/shm/{rx.name}", "r+b") as f:
+        m = mmap.mmap(f.fileno(), 4096)
+        struct.pack_into("<I", m, 64, start)
+        struct.pack_into("<I", m, 128, start)
+        sent = [payload(2, 20 + i, (2, 4, 1, 16), 70 + i) for i in range(6)]  # 4 page chunks each
+        t = threading.Thread(target=lambda: [tx.send_host(p, b"w%d" % i, timeout=10) for i, p in enumerate(sent)])
+        t.start()
+        for i, p in enumerate(sent):
+            h = rx.recv_header(timeout=10)
+            assert h.meta == b"w%d" % i
+            out = torch.empty_like(p)
+            rx.recv_host(out, timeout=10)
+            assert torch.equal(out.view(torch.int16), p.view(torch.int16)), f"message {i}"
+        t.join()
+        head, tail = struct.unpack_from("<I", m, 64)[0], struct.unpack_from("<I", m, 128)[0]
+        m.close()
+    assert head == tail and head < 64          # both counters wrapped past 2^32
+    tx.close()
+    rx.close()
+
+
 def test_threads_share_an_endpoint_message_by_message():
     # Four receiving threads take whole messages from one endpoint with
     # message(); every message arrives exactly once, whole.
-    tx, rx = pair(slot_bytes=4096, num_slots=3)
+    tx, rx = pair(slot_bytes=4096, num_slots=8)
     sent = {f"m{i}".encode(): payload(2, 3 + i, (2, 4, 1, 16), 50 + i) for i in range(12)}
     got, errors = {}, []
 

@@ -88,7 +88,7 @@ def test_device_to_device_through_the_ring(gpu, L, pages, shape, n, slot):
         rx.recv(dst, d_ids, timeout=30)
         torch.cuda.synchronize()
 
-    msg = run_pair(slot, 3, lambda tx: tx.send(src, s_ids, b"pages", timeout=30), recv)
+    msg = run_pair(slot, 4, lambda tx: tx.send(src, s_ids, b"pages", timeout=30), recv)
     assert msg >= 1
     si, di = torch.tensor(s_ids, device=gpu), torch.tensor(d_ids, device=gpu)
     keep = torch.tensor(sorted(set(range(pages)) - set(d_ids)), device=gpu, dtype=torch.long)
@@ -226,7 +226,7 @@ def test_worker_send_and_receive(gpu, tokens_src, tokens_dst):
     def recv(rx):
         got["status"] = dst_w._recv_kv_cache(dst_seq, rx, gpu, timeout=30)
 
-    ref, rank = run_pair(1 << 20, 3, lambda tx: src_w._send_kv_cache(seq, tx, 1.0, 2.0), recv)
+    ref, rank = run_pair(1 << 20, 4, lambda tx: src_w._send_kv_cache(seq, tx, 1.0, 2.0), recv)
     assert isinstance(ref, KVref) and ref.kv_indices == src_table and rank == 0
     assert ref.size == L * len(src_table) * 2 * P * H * D * 2 / 1e6
     assert src_w.seq_manager.block_manager.get_num_free_gpu_blocks() == free_before + len(src_table)
@@ -290,7 +290,7 @@ def test_insertion_threads_share_one_channel(gpu):
             tx.send_host(torch.empty((0, 0, 2, P, H, D), dtype=torch.float16),
                          KVref(f"stop{i}", [], 0.0).meta(), timeout=30)
 
-    run_pair(1 << 20, 3, send, recv)
+    run_pair(1 << 20, 4, send, recv)
     assert not errors, errors
     for s in seqs:
         st = results[s.seq_id]
