@@ -210,6 +210,8 @@ def run_device(args, w, dev, src, dst, plan, s_ids, d_ids):
             "traffic": None,
             "kernel": copy_kernel_names(args.mode, w.shape.page_bytes),
             "algorithmic_bytes_per_launch": int(statistics.mean(bytes_per_launch)),
+            # page ids read per launch (one int32 per page; not in `achieved`)
+            "block_table_bytes_per_launch": 4 * n,
             "mean_launch_us": round(mean_launch_ms * 1e3, 2),
             "launch_timing": "HIP events around the K timed steps on the launch stream, divided by "
                              "the launches they hold",
