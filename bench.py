@@ -735,7 +735,7 @@ def run_promote(dev, steps=100, warmup=10):
         mig = migrate.KVMigrator(src, dst, alloc)
         kind = mode.replace("_native", "")
         lat = []
-        n_iter = warmup + (steps if mode != "pinned" else max(20, steps // 5))
+        n_iter = warmup + steps
         for i in range(n_iter):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
@@ -760,7 +760,7 @@ def run_promote(dev, steps=100, warmup=10):
     for name, fn in (("swap_out", lambda: ops.swap_out(dpool, w.src_tables[0], hpool, hids)),
                      ("swap_in", lambda: ops.swap_in(hpool, hids, ops.PagedPool(dst), w.src_tables[0]))):
         lat = []
-        for i in range(warmup + max(20, steps // 5)):
+        for i in range(warmup + steps):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             fn()
@@ -768,7 +768,7 @@ def run_promote(dev, steps=100, warmup=10):
             if i >= warmup:
                 lat.append((time.perf_counter() - t0) * 1e6)
         lat.sort()
-        out[name] = {"p50_us": round(statistics.median(lat), 1),
+        out[name] = {"p50_us": round(statistics.median(lat), 1), "p90_us": round(lat[int(0.9 * (len(lat) - 1))], 1),
                      "gbs": round(w.payload_bytes / (statistics.median(lat) * 1e-6) / 1e9, 2), "runs": len(lat)}
         log(f"promote 4096 tok {name}: p50 {out[name]['p50_us']} us ({out[name]['gbs']} GB/s)")
     out["payload_bytes"] = w.payload_bytes
