@@ -972,6 +972,50 @@ def summarize_stats(stats_csv: str, bench_json: str, command: str, trace_csv: st
     return "\n".join(out) + "\n"
 
 
+def summarize_promote(trace_csv: str, bench_json: str, command: str) -> str:
+    """Markdown summary of the promote kernels in a rocprofv3 kernel trace of
+    one bench.py run.  pace_kv_promote carries a 4096-token request's page ids
+    in the kernel arguments, so its launches are the run's only
+    page_copy_inline_kernel dispatches: a pack (source ids inline) and an
+    unpack (destination ids inline) per buffer-mode promote, one move (both
+    inline) per fused promote."""
+    bench = _json(bench_json)
+    pr = bench["promote_4k"]
+    kinds = {"true, false>": "pack (source ids inline)", "false, true>": "unpack (destination ids inline)",
+             "true, true>": "move (both inline)"}
+    durs = {}
+    for r in _rows(trace_csv):
+        name = r["Kernel_Name"]
+        if "page_copy_inline_kernel" not in name:
+            continue
+        tmpl = name.split("page_copy_inline_kernel<", 1)[1].split(">", 1)[0] + ">"
+        kind = next((v for k, v in kinds.items() if tmpl.endswith(k)), tmpl)
+        durs.setdefault(kind, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    payload = pr["payload_bytes"]
+    out = ["# promote kernels on llama3-8b-4096tok-bf16 - kernel trace", "",
+           "One 4096-token request (256 pages), Llama-3-8B KV, bf16, 2048-page pools; "
+           f"payload {payload} B. `pace_kv_promote` plans, allocates and launches in one call.", "",
+           "Command (repo root, one MI355X):", "", "```", "export TMPDIR=/tmp", command, "```", "",
+           "| kernel | launches | mean us | p50 us | min us | max us | GB/s (2 x payload / p50) |",
+           "|---|---|---|---|---|---|---|"]
+    for kind in ("pack (source ids inline)", "unpack (destination ids inline)", "move (both inline)"):
+        d = sorted(durs.get(kind, []))
+        if not d:
+            continue
+        p50 = statistics.median(d)
+        out.append(f"| {kind} | {len(d)} | {statistics.mean(d):.1f} | {p50:.1f} | {d[0]:.1f} | {d[-1]:.1f} | "
+                   f"{2 * payload / (p50 * 1e-6) / 1e9:.0f} |")
+    pk = statistics.median(durs.get("pack (source ids inline)", [0.0]))
+    up = statistics.median(durs.get("unpack (destination ids inline)", [0.0]))
+    mv = statistics.median(durs.get("move (both inline)", [0.0]))
+    out += ["", f"bench.py in the same run: promote p50 {pr['buffer_native']['p50_us']} us (pack + unpack, "
+            f"{pr['buffer_native']['runs']} runs), of which {pk + up:.1f} us are the two kernels "
+            f"({4 * payload / ((pk + up) * 1e-6) / 1e9:.0f} GB/s of pack+unpack bytes); fused promote p50 "
+            f"{pr['fused_native']['p50_us']} us, of which {mv:.1f} us is the move kernel. The rest is host "
+            f"time (Python, planning, launch) and completion."]
+    return "\n".join(out) + "\n"
+
+
 def summarize_copies(copy_csv: str, kernel_csv: str, bench_json: str, command: str) -> str:
     """Markdown summary of the pinned-host round trip from a rocprofv3
     --memory-copy-trace (DMA-engine copies) and --kernel-trace (the runtime
@@ -1087,6 +1131,10 @@ def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-stats":
         # python bench.py --summarize-stats KERNEL_STATS.csv BENCH_LINE.json "COMMAND" [KERNEL_TRACE.csv]
         print(summarize_stats(*sys.argv[2:6]), end="")
+        return
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-promote":
+        # python bench.py --summarize-promote KERNEL_TRACE.csv BENCH_LINE.json "COMMAND"
+        print(summarize_promote(sys.argv[2], sys.argv[3], sys.argv[4]), end="")
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-copies":
         # python bench.py --summarize-copies MEMORY_COPY_TRACE.csv KERNEL_TRACE.csv BENCH_LINE.json "COMMAND"

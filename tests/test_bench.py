@@ -101,3 +101,25 @@ def test_more_than_one_gpu_is_refused():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
+
+
+def test_summarize_promote_splits_the_inline_kernels(tmp_path):
+    inline = "void pace_kv::(anonymous namespace)::page_copy_inline_kernel<false, {}, true, {}, {}>(x)"
+    rows, t = [], 0
+    for i, (pack, s_in, d_in, dur) in enumerate([("true", "true", "false", 150000),
+                                                  ("false", "false", "true", 152000)] * 3
+                                                 + [("false", "true", "true", 165000)] * 2):
+        rows.append({"Dispatch_Id": i + 1, "Kernel_Name": inline.format(pack, s_in, d_in),
+                     "Start_Timestamp": t, "End_Timestamp": t + dur})
+        t += dur + 1000
+    rows.append({"Dispatch_Id": 99, "Kernel_Name": COPY, "Start_Timestamp": 0, "End_Timestamp": 7})
+    path = write_csv(tmp_path / "k.csv", rows)
+    b = {"promote_4k": {"payload_bytes": 1 << 29, "buffer_native": {"p50_us": 327.0, "runs": 3},
+                        "fused_native": {"p50_us": 186.0, "runs": 2}}}
+    bj = tmp_path / "b.json"
+    bj.write_text(json.dumps(b))
+    md = bench.summarize_promote(path, str(bj), "CMD")
+    assert "| pack (source ids inline) | 3 | 150.0 | 150.0 |" in md
+    assert "| unpack (destination ids inline) | 3 | 152.0 | 152.0 |" in md
+    assert "| move (both inline) | 2 | 165.0 | 165.0 |" in md
+    assert "of which 302.0 us are the two kernels" in md and "of which 165.0 us is the move kernel" in md
