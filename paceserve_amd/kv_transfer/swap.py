@@ -74,17 +74,19 @@ class SwapSpace:
             self._swap_in(seq_id, dev_table)
 
     def _swap_in(self, seq_id: str, dev_table: List[int]) -> None:
-        host_table = self.tables.pop(seq_id)
+        # Nothing changes until the copy is enqueued: a rejected call leaves
+        # the request swapped out, its host pages held.
+        host_table = self.tables[seq_id]
         ids = normalize_page_ids(dev_table, self.dev.num_pages)
         if len(ids) != len(host_table):
-            self.tables[seq_id] = host_table
             raise ValueError(f"{len(ids)} device pages for {len(host_table)} swapped pages")
         stream = torch.cuda.current_stream(self.dev.device)
-        stream.wait_event(self._swapped_out.pop(seq_id))
+        stream.wait_event(self._swapped_out[seq_id])
         ops.swap_in(self.host, host_table, self.dev, ids)
         ev = torch.cuda.Event()
         ev.record(stream)
         self._swapped_in = ev
+        del self.tables[seq_id], self._swapped_out[seq_id]
         self.host_allocator.free_many(host_table)
 
     def holds(self, seq_id: str) -> bool:

@@ -142,6 +142,27 @@ def test_swap_space_preemption_round_trip(gpu):
         space.swap_in("req-1", new_table)
 
 
+def test_swap_space_rejected_swap_in_keeps_the_request(gpu):
+    # A swap-in refused before its copy (a bad device id, a short table)
+    # leaves the request swapped out with its host pages; a correct call
+    # then brings the pages back.
+    dev = dev_pool(gpu, 32, 9)
+    space = SwapSpace(dev, 16)
+    table = [3, 7, 11]
+    saved = [words(t[torch.tensor(table, device=gpu)]).clone() for t in dev.layers]
+    space.swap_out("req-x", table)
+    with pytest.raises(IndexError):
+        space.swap_in("req-x", [1, 2, 99])
+    with pytest.raises(ValueError):
+        space.swap_in("req-x", [1, 2])
+    assert space.holds("req-x") and space.num_free_host_pages() == 13
+    space.swap_in("req-x", [20, 21, 22])
+    torch.cuda.synchronize()
+    assert not space.holds("req-x") and space.num_free_host_pages() == 16
+    for l in range(SHAPE.num_layers):
+        assert torch.equal(words(dev.layers[l][torch.tensor([20, 21, 22], device=gpu)]), saved[l])
+
+
 def test_swap_space_orders_work_across_streams(gpu):
     # Swap out on one stream and in on another with no host synchronisation:
     # the swap-in waits for the swap-out that wrote its host pages, and a
