@@ -262,6 +262,12 @@ class KVMigrator:
             return MigrationPlan(src_ids.tolist(), dst_ids, dst_tables, indptr.tolist())
         plan = self.plan(src_tables, dst_pages)
         if plan.n_pages:
-            s_ids, d_ids = self.upload(plan)
-            self.move_pages(s_ids, d_ids, mode, layers_per_chunk, host_buf)
+            try:
+                s_ids, d_ids = self.upload(plan)
+                self.move_pages(s_ids, d_ids, mode, layers_per_chunk, host_buf)
+            except BaseException:
+                # Undo the allocation exactly (pages go back in reverse pop
+                # order), as the native promotion does on failure.
+                self.dst_allocator.free_many(reversed([p for t in plan.dst_tables for p in t]))
+                raise
         return plan

@@ -91,6 +91,24 @@ def test_native_promote_out_of_pages_leaves_allocator_unchanged(gpu):
         assert torch.equal(words(dst8.layers[l]), before[l])
 
 
+@pytest.mark.parametrize("native", [False, True])
+def test_failed_copy_returns_the_destination_pages(gpu, native):
+    # A pinned-host promotion whose host buffer is smaller than one layer
+    # chunk is refused by the round trip after the plan allocated its pages:
+    # the pages go back and the free list is exactly as before.
+    src, dst = pools(gpu, 17)
+    free = np.random.default_rng(5).permutation(POOL).tolist()
+    alloc = (NativeBlockAllocator if native else BlockAllocator)(SHAPE.page_size, POOL, free_list=free)
+    before = list(alloc.free_blocks)
+    mig = migrate.KVMigrator(src, dst, alloc)
+    tables = [list(range(0, 40)), list(range(100, 130))]
+    tiny = torch.empty(1024, dtype=torch.uint8, pin_memory=True)
+    with pytest.raises(Exception):
+        mig.promote(tables, mode="pinned", host_buf=tiny)
+    torch.cuda.synchronize()
+    assert list(alloc.free_blocks) == before
+
+
 def test_one_migrator_from_threads_on_their_own_streams(gpu):
     # Two threads promote through one migrator (its transfer buffer is
     # shared) on streams of their own, with no host synchronisation between.
