@@ -204,10 +204,16 @@ class KVChannel:
         return out
 
     def discard(self, timeout: float = 60.0) -> None:
-        """Drains the current message's payload without keeping it."""
+        """Drains the current message's payload without keeping it.  A message
+        whose receive the library already gave up (the sender abandoned it, or
+        a device step failed) has nothing left to drain: its leftover chunks
+        are skipped before the next header.  Other failures (a timeout) keep
+        the message pending, so that the drain can be retried."""
         if self._header is None:
             return
-        _native.check(_native.load().pace_kv_channel_recv_host(self._require(), None, 0, _ms(timeout)))
+        rc = _native.load().pace_kv_channel_recv_host(self._require(), None, 0, _ms(timeout))
+        if rc != _native.PACE_KV_ESTATE:
+            _native.check(rc)
         self._header = None
 
     def _current(self) -> MessageHeader:

@@ -189,6 +189,40 @@ def test_abandoned_message_fails_the_receiver_and_the_channel_recovers():
     rx.close()
 
 
+def test_message_context_reports_the_receive_error():
+    # An abandoned message taken with message(): the caller sees the
+    # receive's own error (the sender abandoned the message), not one from
+    # the clean-up drain, and the endpoint then takes the next message.
+    tx, rx = pair(slot_bytes=4096, num_slots=2)
+    big = payload(2, 64, (2, 4, 1, 16), 3)         # 16 chunks through 2 slots
+    errs = []
+
+    def send():
+        try:
+            tx.send_host(big, b"big", timeout=0.3)
+        except _native.PaceKVError as exc:
+            errs.append(exc.status)
+
+    t = threading.Thread(target=send)
+    t.start()
+    with pytest.raises(_native.PaceKVError) as e:
+        with rx.message(timeout=10) as h:
+            assert h.meta == b"big"
+            t.join(timeout=10)                       # the sender gives up
+            rx.recv_host(torch.empty_like(big), timeout=5)
+    assert errs == [_native.PACE_KV_ETIMEDOUT]
+    assert status(e) == _native.PACE_KV_ESTATE and "abandoned" in str(e.value)
+    small = payload(1, 2, (2, 4, 1, 16), 4)
+    t = threading.Thread(target=lambda: tx.send_host(small, b"next", timeout=10))
+    t.start()
+    with rx.message(timeout=10) as h:
+        out = rx.recv_host(torch.empty_like(small), timeout=10)
+    t.join()
+    assert h.meta == b"next" and torch.equal(out.view(torch.int16), small.view(torch.int16))
+    tx.close()
+    rx.close()
+
+
 def test_discarded_payload_leaves_the_next_message_intact():
     tx, rx = pair(slot_bytes=4096, num_slots=2)
     a, b = payload(3, 30, (2, 4, 1, 16), 5), payload(2, 3, (2, 4, 1, 16), 6)
