@@ -107,8 +107,9 @@ struct alignas(64) ChannelCtl {
 // head and tail count records modulo 2^32 and a record's slot is the count
 // modulo num_slots; a power-of-two slot count divides 2^32, so consecutive
 // records keep consecutive slots across the counters' wrap.
-static_assert(offsetof(ChannelCtl, head) == 64 && offsetof(ChannelCtl, tail) == 128,
-              "control-block layout (the wrap test sets head and tail at these offsets)");
+static_assert(offsetof(ChannelCtl, num_slots) == 12 && offsetof(ChannelCtl, head) == 64 &&
+                  offsetof(ChannelCtl, tail) == 128,
+              "control-block layout (the CPU tests write num_slots, head and tail at these offsets)");
 
 bool valid_slot_count(int64_t n) { return n >= 2 && n <= kMaxSlots && (n & (n - 1)) == 0; }
 

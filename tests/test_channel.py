@@ -345,6 +345,25 @@ def test_record_counters_wrap_at_2_32():
     rx.close()
 
 
+def test_open_refuses_a_slot_count_that_is_not_a_power_of_two():
+    # The opener checks the control block too: a ring whose num_slots (byte
+    # 12) is not a power of two is refused as incompatible.
+    import mmap
+    import struct
+
+    nm = name()
+    rx = KVChannel.create(nm, 4096, 4, 1)
+    with open(f"/dev/shm/{nm}", "r+b") as f:
+        m = mmap.mmap(f.fileno(), 4096)
+        assert struct.unpack_from("<I", m, 12)[0] == 4
+        struct.pack_into("<I", m, 12, 3)
+        m.close()
+    with pytest.raises(_native.PaceKVError) as e:
+        KVChannel.open(nm, 1, timeout=1)
+    assert status(e) == _native.PACE_KV_ESTATE and "incompatible" in str(e.value)
+    rx.close()
+
+
 def test_threads_share_an_endpoint_message_by_message():
     # Four receiving threads take whole messages from one endpoint with
     # message(); every message arrives exactly once, whole.
