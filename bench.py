@@ -1,25 +1,29 @@
 """Benchmark of the KV-cache migration hot path on one MI355X.
 
-Default workload (N=1): llama3-8b-16req-bf16 - 16 requests with
-lognormal(median 1024, sigma 1.0) token counts clipped to [128, 8192],
-Llama-3-8B KV shape (32 layers, 8 KV heads, head_dim 128, page 16), bf16,
-16384-page source and destination pools, fragmented source free list.  One step = pack every
-request's pages from all layers into the contiguous transfer buffer, then
-unpack the buffer into the destination pages (the reference's
+Default workload (N=1): llama3-70b-256req-bf16, the largest of the five
+migration workloads and one that fits one GPU - 256 requests of U{64..2048}
+tokens at the Llama-3-70B KV shape (80 layers, 8 KV heads, head_dim 128, page
+16), bf16, 20480-page source and destination pools with the source pages dealt
+to requests round-robin (heavily fragmented), moved in 8-layer chunks.  One
+step = pack every request's pages from all layers into the contiguous transfer
+buffer, then unpack the buffer into the destination pages (the reference's
 get_kv_cache + insert_kv_cache, moved on-device).
 
 value = 4 * payload / elapsed, in GB/s (1e9 B/s): pack reads and writes the
 payload, unpack reads and writes it; elapsed is measured with HIP events on
 the stream the kernels run on, over the K timed steps.  Inputs are resident in
-HBM before timing starts.  Also reported: the roofline of the copy kernel
-(algorithmic bytes per launch / mean launch time vs 8 TB/s), p50/p90 promote
-latency of one 4096-token request (dst allocation + remap + block-table H2D +
-pack + unpack, to completion) and the reference's CPU path (torch
-index_select / index_copy_ on host tensors) timed on a bounded sample on this
-host's cores.
+HBM before timing starts.  After the timed steps every layer of both pools is
+compared byte for byte with torch's own gather/scatter of the same pages
+(`verified`).  Also reported: the roofline of the copy kernel (algorithmic
+bytes per launch / mean launch time vs 8 TB/s), the other four workloads in the
+same process (`configs`: GB/s, fraction of peak and the same exact check; the
+pinned-host legs of the two that have one, `staging`), p50/p90 promote latency
+of one 4096-token request (dst allocation + remap + block-table H2D + pack +
+unpack, to completion) and the reference's CPU path (torch index_select /
+index_copy_ on host tensors) timed on a bounded sample on this host's cores.
 
 Usage: python bench.py [--steps K] [--warmup W] [--workload NAME]
-       [--no-cpu] [--no-promote] [--verify]
+       [--no-cpu] [--no-promote] [--no-verify] [--no-configs]
 (NAME: one of paceserve_amd.workloads.NAMES; see that module)
 """
 from __future__ import annotations
@@ -59,7 +63,11 @@ def parse_args():
                     help="buffer: pack + unpack (the metric); fused: pool-to-pool move")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-promote", action="store_true")
-    ap.add_argument("--verify", action="store_true", help="check the result against torch's gather/scatter")
+    ap.add_argument("--no-verify", dest="verify", action="store_false",
+                    help="skip the exact check of both pools against torch's gather/scatter")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other workloads (timed, checked and, where they have one, staged after the "
+                         "headline workload)")
     ap.add_argument("--cpu-layers", type=int, default=0, help="layers in the CPU sample (0 = auto)")
     ap.add_argument("--calibrate", action="store_true",
                     help="after timing, run torch's contiguous copy of 1 GiB three times (PMC scale reference)")
@@ -80,12 +88,11 @@ def parse_args():
 def device_setup(w, dev):
     import torch
 
-    from paceserve_amd import workloads
     from paceserve_amd.core.block_manager import BlockAllocator
     from paceserve_amd.kv_transfer import migrate, ops
 
-    src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev)
-    dst = workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev)
+    src = w.src_pool(dev)
+    dst = w.dst_pool(dev)
     alloc = BlockAllocator(w.shape.page_size, w.dst_pool_pages, w.dst_free)
     plan = migrate.plan_batch(w.src_tables, w.src_pool_pages, alloc)
     s_ids = torch.tensor(plan.src_ids, dtype=torch.int32, device=dev)
@@ -452,8 +459,8 @@ def run_dropin(dev, steps: int = 10, warmup: int = 2) -> dict:
 
     w = workloads.get(workloads.PROMOTE)
     L, n = w.shape.num_layers, w.n_pages
-    src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev)
-    dst = workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev)
+    src = w.src_pool(dev)
+    dst = w.dst_pool(dev)
     ids = list(w.src_tables[0])
     dst_ids = list(range(w.dst_pool_pages - 1, w.dst_pool_pages - 1 - n, -1))   # a fresh LIFO pool's pages
 
@@ -533,7 +540,7 @@ def channel_sender(name: str) -> None:
     _native.load()
     dev = torch.device("cuda", 0)
     w = workloads.get(workloads.PROMOTE)
-    src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev)
+    src = w.src_pool(dev)
     torch.cuda.synchronize()
     ids = list(w.src_tables[0])
     with KVChannel.open(name, CHANNEL_THREADS, timeout=120) as ch:
@@ -571,7 +578,7 @@ def run_channel(dev, runs: int = 10, warmup: int = 2, ref_runs: int = 3) -> dict
     child = subprocess.Popen([sys.executable, str(ROOT / "bench.py"), "--channel-sender", name],
                              stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True)
     try:
-        dst = ops.PagedPool(workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev))
+        dst = ops.PagedPool(w.dst_pool(dev))
         d_ids = ops.device_ids(dst_ids, dev)
         if child.stdout.readline().strip() != "ready":
             raise RuntimeError("channel sender did not start")
@@ -596,7 +603,7 @@ def run_channel(dev, runs: int = 10, warmup: int = 2, ref_runs: int = 3) -> dict
             child.kill()
         ch.close()
     ms = statistics.median(ts) * 1e3
-    src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev)
+    src = w.src_pool(dev)
     si, di = torch.tensor(ids, device=dev), torch.tensor(dst_ids, device=dev)
     ok = all(torch.equal(d[di].view(torch.int16), s[si].view(torch.int16)) for d, s in zip(dst.layers, src))
     out = {"payload_bytes": w.payload_bytes, "workload": w.name, "runs": runs,
@@ -605,8 +612,7 @@ def run_channel(dev, runs: int = 10, warmup: int = 2, ref_runs: int = 3) -> dict
            "channel_p90_ms": round(sorted(ts)[int(0.9 * (len(ts) - 1))] * 1e3, 2), "same_bytes": ok}
     log(f"channel: {ms:.2f} ms per request across processes, {out['channel_gbs']} GB/s, same bytes {ok}")
     del dst
-    torch.cuda.empty_cache()
-    dst = workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev)
+    dst = w.dst_pool(dev)
     rts = []
     for r in range(1 + ref_runs):
         torch.cuda.synchronize()
@@ -627,8 +633,6 @@ def run_channel(dev, runs: int = 10, warmup: int = 2, ref_runs: int = 3) -> dict
                                  "(per layer), one process; excludes Ray's RPCs and object-store copies")
     out["speedup_vs_reference_emulated"] = round(rms / ms, 2)
     log(f"channel reference path (emulated): {rms:.2f} ms")
-    del src, dst
-    torch.cuda.empty_cache()
     return out
 
 
@@ -704,15 +708,74 @@ def run_staging(w, dev, src, dst, s_ids, d_ids, reps: int = 3):
 
 
 def verify(w, src, dst, s_ids, d_ids, dev) -> bool:
-    """Destination pages equal the source pages torch's own gather selects."""
-    import torch
+    """Every layer of both pools, byte for byte: the destination equals its
+    content before the migration (regenerated from its seed) with torch's
+    index_copy_ of the index_select'ed source pages applied, and the source
+    equals its content before (workloads.migration_mismatch)."""
+    from paceserve_amd import workloads
 
-    for l in range(w.shape.num_layers):
-        a = src.layers[l].index_select(0, s_ids.long()).view(torch.int16)
-        b = dst.layers[l].index_select(0, d_ids.long()).view(torch.int16)
-        if not torch.equal(a, b):
-            return False
-    return True
+    bad = workloads.migration_mismatch(src.layers, dst.layers, s_ids, d_ids, w.dst_before(dev), w.src_before(dev))
+    if bad is not None:
+        log(f"{w.name}: verification failed: {bad}")
+    return bad is None
+
+
+VERIFIED_WHAT = ("every layer of both pools compared byte for byte: destination = its seeded content before "
+                 "with torch index_copy_(dst_ids, index_select(src, src_ids)) applied; source unchanged")
+
+
+def config_steps(w, steps: int, seconds: float = 0.05) -> int:
+    """Timed steps for a workload measured beside the headline: at least
+    `steps`, and enough for about `seconds` of copying at 6.5 TB/s, so that the
+    events around the timed region stay negligible on small payloads."""
+    est = 4 * w.payload_bytes / 6.5e12
+    return max(steps, min(2000, int(seconds / est) + 1))
+
+
+CPU_CONFIG_SECONDS = 3.0
+CPU_CONFIG_LAYERS = 4
+
+
+def run_config(args, name: str, dev) -> dict:
+    """One of the other workloads, measured in the same process after the
+    headline: K timed steps of pack + unpack (value and roofline as for the
+    headline), the exact check of both pools, the pinned-host legs when the
+    workload has them (checked again after), the identity-id copy ceiling
+    (last: it writes pages no id names) and a short CPU sample."""
+    import argparse
+
+    from paceserve_amd import workloads
+
+    w = workloads.get(name)
+    log(f"config {w.name}: {w.description}")
+    src, dst, plan, s_ids, d_ids = device_setup(w, dev)
+    sub = argparse.Namespace(**vars(args))
+    sub.steps = config_steps(w, args.steps)
+    sub.mode = "buffer"
+    res = run_device(sub, w, dev, src, dst, plan, s_ids, d_ids)
+    out = {"config": w.summary(), "value": round(res["value"], 1), "unit": "GB/s",
+           "frac_of_hbm_peak": round(res["value"] / HBM_PEAK_GBS, 4), "steps": sub.steps, "warmup": args.warmup,
+           "ms_per_step": round(res["event_ms_per_step"], 4), "pack_ms": res["pack_ms_mean"],
+           "unpack_ms": res["unpack_ms_mean"], "roofline": res["roofline"]}
+    log(f"config {w.name}: {out['value']} GB/s ({out['frac_of_hbm_peak'] * 100:.1f}% of peak), K={sub.steps}")
+    if args.verify:
+        out["verified"] = verify(w, src, dst, s_ids, d_ids, dev)
+        log(f"config {w.name}: verified {out['verified']}")
+    if not args.no_staging and w.staging in ("pinned", "both"):
+        settle = link_settle(dev)
+        st = run_staging(w, dev, src, dst, s_ids, d_ids)
+        st["link_probe"] = settle
+        st["workload"] = w.name
+        out["staging"] = st
+        if args.verify:
+            out["verified_after_staging"] = verify(w, src, dst, s_ids, d_ids, dev)
+            log(f"config {w.name}: verified after staging {out['verified_after_staging']}")
+    out["copy_ceiling"] = run_ceiling(w, dev, src, dst, plan.n_pages)
+    if not args.no_cpu:
+        layers = min(CPU_CONFIG_LAYERS, cpu_sample_layers(w))
+        out["cpu_baseline"] = run_cpu_baseline(w, layers, src, dst, plan, CPU_CONFIG_SECONDS)
+        log(f"config {w.name}: CPU baseline {out['cpu_baseline']['value']} GB/s")
+    return out
 
 
 def run_promote(dev, steps=100, warmup=10):
@@ -724,8 +787,8 @@ def run_promote(dev, steps=100, warmup=10):
     from paceserve_amd.kv_transfer import migrate
 
     w = workloads.get(workloads.PROMOTE)
-    src = workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, dev)
-    dst = workloads.fill_pool(w.dst_pool_pages, w.shape, w.seed + 50, w.init, dev)
+    src = w.src_pool(dev)
+    dst = w.dst_pool(dev)
     host = torch.empty(w.payload_bytes, dtype=torch.uint8, pin_memory=True)
     out = {}
     # "buffer"/"fused": Python planner + ops; "*_native": one pace_kv_promote call
@@ -809,7 +872,7 @@ def run_calibration(dev) -> None:
 CPU_SAMPLE_SECONDS = 10.0
 
 
-def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan):
+def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan, seconds: float = None):
     """The reference's CPU path on pageable host tensors: per layer,
     index_select into the buffer then index_copy_ into the destination.  The
     host pools are copies of the first layers of the device pools (same
@@ -828,9 +891,9 @@ def run_cpu_baseline(w, layers_sample: int, src_pool, dst_pool, plan):
     buf = torch.empty((L, plan.n_pages) + w.shape.page_shape, dtype=w.shape.dtype)
     for _ in range(2):                                                # warm-up (first touch)
         orc.torch_cpu_pack_unpack(src, s_idx, dst, d_idx, buf)
-    # Passes until CPU_SAMPLE_SECONDS of work are timed (5 to 5000 passes).
+    # Passes until `seconds` (CPU_SAMPLE_SECONDS) of work are timed (5 to 5000 passes).
     times = []
-    end = time.perf_counter() + CPU_SAMPLE_SECONDS
+    end = time.perf_counter() + (CPU_SAMPLE_SECONDS if seconds is None else seconds)
     while len(times) < 5 or (len(times) < 5000 and time.perf_counter() < end):
         t0 = time.perf_counter()
         orc.torch_cpu_pack_unpack(src, s_idx, dst, d_idx, buf)
@@ -1073,7 +1136,7 @@ def pmc_markdown(traffic_json: str) -> str:
     chunk = min(w.device_layers_per_chunk or w.shape.num_layers, w.shape.num_layers)
     alg = 2 * chunk * w.n_pages * w.shape.page_bytes
     run = (f"python3 bench.py --workload {wl} --no-cpu --no-promote --no-staging --no-dropin --no-append --no-channel "
-           "--steps 3 --warmup 1 --calibrate")
+           "--no-configs --no-verify --steps 3 --warmup 1 --calibrate")
     # the counter runs wrote their CSVs (<dir>/f_counter_collection.csv and
     # <dir>/w_counter_collection.csv) where the summary read them
     fdir = os.path.dirname(t.get("fetch_csv", f"pmc_fetch_{wl}/f_counter_collection.csv"))
@@ -1162,11 +1225,8 @@ def main():
     if args.verify:
         res["verified"] = verify(w, src, dst, s_ids, d_ids, dev)
         log(f"verified: {res['verified']}")
-    ceiling = run_ceiling(w, dev, src, dst, plan.n_pages) if args.mode == "buffer" else None
     torch_dev = run_torch_device(w, dev, src, dst, s_ids, d_ids)
     append = None if args.no_append else run_append(dev)
-    if args.calibrate:
-        run_calibration(dev)
     cpu = None
     if not args.no_cpu:
         layers = args.cpu_layers or cpu_sample_layers(w)
@@ -1184,23 +1244,37 @@ def main():
         if want_staging:
             staging = run_staging(w, dev, src, dst, s_ids, d_ids)
             staging["link_probe"] = settle
+            staging["workload"] = w.name
             if args.verify:
                 res["verified_after_staging"] = verify(w, src, dst, s_ids, d_ids, dev)
         if not args.no_promote:
             promote = run_promote(dev)
             promote["link_probe"] = settle
+    # The identity-id ceiling writes destination pages that no id names, so it
+    # runs after every check of the pools; the calibration copies come last.
+    ceiling = run_ceiling(w, dev, src, dst, plan.n_pages) if args.mode == "buffer" else None
+    if args.calibrate:
+        run_calibration(dev)
     dropin = None
     if not args.no_dropin:
         settle = link_settle(dev)       # the promote leg has just freed its pools
         dropin = run_dropin(dev)
         dropin["link_probe"] = settle
+    # Memory freed from here on stays in torch's cache for the later legs and
+    # workloads (no empty_cache): memory returned to the driver is scrubbed
+    # with the DMA engines the host legs use, which halved the staging rates
+    # of workloads measured after a freed 215 GB pool pair.
     del src, dst, s_ids, d_ids
-    torch.cuda.empty_cache()
     channel = None
     if not args.no_channel:
         settle = link_settle(dev)
         channel = run_channel(dev)
         channel["link_probe"] = settle
+    configs = None
+    if not args.no_configs:
+        configs = {name: run_config(args, name, dev) for name in workloads.NAMES if name != w.name}
+    if staging is None and configs:
+        staging = next((c["staging"] for c in configs.values() if "staging" in c), None)
 
     line = {
         "metric": METRIC,
@@ -1230,6 +1304,7 @@ def main():
         "dropin": dropin,
         "channel": channel,
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     tr = traffic_from_profiles(w.name) if args.mode == "buffer" else None
     if tr is not None:
@@ -1238,6 +1313,11 @@ def main():
     for key in ("verified", "verified_after_staging"):
         if key in res:
             line[key] = res[key]
+    if "verified" in res:
+        line["verified_what"] = VERIFIED_WHAT
+    if configs:
+        line["configs_summary"] = {name: {"value": c["value"], "frac": c["frac_of_hbm_peak"],
+                                          "verified": c.get("verified")} for name, c in configs.items()}
     print(json.dumps(line), flush=True)
 
 

@@ -178,6 +178,9 @@ class BlockSpaceManager:
         cls = NativeBlockAllocator if native else BlockAllocator
         self.gpu_allocator = cls(block_size, num_gpu_blocks, free_list)
         self.block_tables: Dict[str, List[int]] = {}
+        # Held by callers that check for room and then allocate, as one step
+        # (several insertion threads share one manager).
+        self.alloc_lock = threading.Lock()
 
     def get_num_initial_blocks(self, seq) -> int:
         return len(seq.logical_token_blocks)

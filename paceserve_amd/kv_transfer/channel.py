@@ -177,7 +177,7 @@ class KVChannel:
         stream; the last ones are still enqueued when the call returns."""
         h = self._current()
         pool = ops.as_pool(dst)
-        ids = ops.device_ids(page_ids, pool.device)
+        ids = ops.device_ids(page_ids, pool.device, distinct=True)
         n = ids.numel()
         if (pool.num_layers, n, pool.page_bytes) != (h.num_layers, h.n_pages, h.page_bytes):
             raise ValueError(f"message {h.msg_id} holds {h.num_layers} layers x {h.n_pages} pages x "

@@ -103,9 +103,14 @@ def as_pool(pool_or_layers) -> PagedPool:
     return pool_or_layers if isinstance(pool_or_layers, PagedPool) else PagedPool(pool_or_layers)
 
 
-def device_ids(ids: IdsLike, device: torch.device) -> torch.Tensor:
+def device_ids(ids: IdsLike, device: torch.device, distinct: bool = False) -> torch.Tensor:
     """Page ids as a contiguous int32 device tensor (host data is copied
-    asynchronously on the current stream through pinned memory)."""
+    asynchronously on the current stream through pinned memory).
+
+    distinct=True (destination ids: two waves copying into one page race,
+    so the page would hold either source) rejects host data that repeats a
+    page with ValueError; device tensors are used as they are, and a caller
+    passing them is responsible for distinct ids."""
     if isinstance(ids, torch.Tensor):
         if ids.device.type == "cuda":
             if ids.dtype != torch.int32 or not ids.is_contiguous() or ids.dim() != 1:
@@ -118,6 +123,11 @@ def device_ids(ids: IdsLike, device: torch.device) -> torch.Tensor:
         host = torch.tensor(list(ids), dtype=torch.int32)
     if host.numel() == 0:
         return torch.empty(0, dtype=torch.int32, device=device)
+    if distinct and host.numel() > 1:
+        u, c = np.unique(host.numpy(), return_counts=True)
+        if (c > 1).any():
+            raise ValueError(f"destination page {int(u[c > 1][0])} appears more than once; destination page "
+                             "ids must be distinct")
     return host.pin_memory().to(device, non_blocking=True)
 
 
@@ -168,10 +178,12 @@ def unpack(buf: torch.Tensor, dst, page_ids: IdsLike, *, layer_begin: int = 0,
            layer_end: Optional[int] = None, err: Optional[torch.Tensor] = None) -> None:
     """dst.layers[l][page_ids[j]] = buf[l - layer_begin, j]; other pages untouched.
 
-    page_ids must not repeat a page (KVhelper removes repeats on the host)."""
+    page_ids must not repeat a page: host ids that do are rejected
+    (ValueError), device ids are the caller's to keep distinct (KVhelper
+    removes repeats on the host, keeping the last write)."""
     pool = as_pool(dst)
     lb, le = pool.layer_range(layer_begin, layer_end)
-    ids = device_ids(page_ids, pool.device)
+    ids = device_ids(page_ids, pool.device, distinct=True)
     n = ids.numel()
     stride = _check_buffer(buf, pool, le - lb, n, "unpack")
     _native.check(_native.load().pace_kv_unpack(
@@ -183,13 +195,14 @@ def unpack(buf: torch.Tensor, dst, page_ids: IdsLike, *, layer_begin: int = 0,
 def move(src, src_ids: IdsLike, dst, dst_ids: IdsLike, *, layer_begin: int = 0,
          layer_end: Optional[int] = None, err: Optional[torch.Tensor] = None) -> None:
     """dst.layers[l][dst_ids[j]] = src.layers[l][src_ids[j]], one fused pass with
-    no transfer buffer (same destination bytes as pack followed by unpack)."""
+    no transfer buffer (same destination bytes as pack followed by unpack).
+    dst_ids must be distinct, as for unpack."""
     sp, dp = as_pool(src), as_pool(dst)
     if not sp.compatible(dp) or sp.num_layers != dp.num_layers:
         raise ValueError("source and destination pools differ in layout, layers, dtype or device")
     lb, le = sp.layer_range(layer_begin, layer_end)
     s_ids = device_ids(src_ids, sp.device)
-    d_ids = device_ids(dst_ids, dp.device)
+    d_ids = device_ids(dst_ids, dp.device, distinct=True)
     if s_ids.numel() != d_ids.numel():
         raise ValueError(f"{s_ids.numel()} source ids but {d_ids.numel()} destination ids")
     n = s_ids.numel()
@@ -200,13 +213,13 @@ def move(src, src_ids: IdsLike, dst, dst_ids: IdsLike, *, layer_begin: int = 0,
         d_ids.data_ptr(), le - lb, n, sp.page_bytes, _err_ptr(err), _stream_handle(sp.device)))
 
 
-def _swap_args(dev: PagedPool, host: PagedPool, dev_ids: IdsLike, host_ids: IdsLike):
+def _swap_args(dev: PagedPool, host: PagedPool, dev_ids: IdsLike, host_ids: IdsLike, into_host: bool):
     if not host.host or dev.host:
         raise ValueError("swap needs one device pool and one host pool")
     if dev.page_shape != host.page_shape or dev.dtype != host.dtype or dev.num_layers != host.num_layers:
         raise ValueError("device and host pools differ in layout, layers or dtype")
-    d_ids = device_ids(dev_ids, dev.device)
-    h_ids = device_ids(host_ids, dev.device)
+    d_ids = device_ids(dev_ids, dev.device, distinct=not into_host)
+    h_ids = device_ids(host_ids, dev.device, distinct=into_host)
     if d_ids.numel() != h_ids.numel():
         raise ValueError(f"{d_ids.numel()} device ids but {h_ids.numel()} host ids")
     return d_ids, h_ids
@@ -217,7 +230,7 @@ def swap_out(dev_pool, dev_ids: IdsLike, host_pool: PagedPool, host_ids: IdsLike
     """host_pool.layers[l][host_ids[j]] = dev_pool.layers[l][dev_ids[j]], one
     kernel writing the pinned host pages across PCIe."""
     dev = as_pool(dev_pool)
-    d_ids, h_ids = _swap_args(dev, host_pool, dev_ids, host_ids)
+    d_ids, h_ids = _swap_args(dev, host_pool, dev_ids, host_ids, into_host=True)
     n = d_ids.numel()
     if n == 0:
         return
@@ -231,7 +244,7 @@ def swap_in(host_pool: PagedPool, host_ids: IdsLike, dev_pool, dev_ids: IdsLike,
     """dev_pool.layers[l][dev_ids[j]] = host_pool.layers[l][host_ids[j]], one
     kernel reading the pinned host pages across PCIe."""
     dev = as_pool(dev_pool)
-    d_ids, h_ids = _swap_args(dev, host_pool, dev_ids, host_ids)
+    d_ids, h_ids = _swap_args(dev, host_pool, dev_ids, host_ids, into_host=False)
     n = d_ids.numel()
     if n == 0:
         return
@@ -366,7 +379,7 @@ class Stager:
                          err: Optional[torch.Tensor] = None) -> None:
         pool = as_pool(dst)
         lb, le = pool.layer_range(layer_begin, layer_end)
-        ids = device_ids(page_ids, pool.device)
+        ids = device_ids(page_ids, pool.device, distinct=True)
         n = ids.numel()
         self._host(host_in, pool, le - lb, n, "unpack_from_host")
         _native.check(_native.load().pace_kv_unpack_from_host(
@@ -381,7 +394,7 @@ class Stager:
         if not sp.compatible(dp) or sp.num_layers != dp.num_layers:
             raise ValueError("source and destination pools differ in layout, layers, dtype or device")
         s_ids = device_ids(src_ids, sp.device)
-        d_ids = device_ids(dst_ids, dp.device)
+        d_ids = device_ids(dst_ids, dp.device, distinct=True)
         if s_ids.numel() != d_ids.numel():
             raise ValueError(f"{s_ids.numel()} source ids but {d_ids.numel()} destination ids")
         n = s_ids.numel()

@@ -12,13 +12,41 @@ back into newly allocated device pages, after which the host pages are free.
 from __future__ import annotations
 
 import threading
-from typing import Dict, List, Optional
+from typing import Dict, List
 
 import torch
 
 from ..core.block_manager import NativeBlockAllocator
 from . import ops
 from .kv_utils import normalize_page_ids
+
+
+class PageReaders:
+    """Which event each host page's last reader (a swap-in) recorded, so that
+    a swap-out writing a page waits for exactly the swap-ins that read it,
+    whichever streams they ran on.  Works with any event object that a
+    stream can wait on; at most one entry per host page."""
+
+    def __init__(self):
+        self._last: Dict[int, object] = {}
+
+    def record(self, pages, event) -> None:
+        for p in pages:
+            self._last[int(p)] = event
+
+    def take(self, pages) -> list:
+        """The distinct events recorded for `pages` (in first-seen order),
+        forgotten: the caller orders its writes after them."""
+        out, seen = [], set()
+        for p in pages:
+            ev = self._last.pop(int(p), None)
+            if ev is not None and id(ev) not in seen:
+                seen.add(id(ev))
+                out.append(ev)
+        return out
+
+    def __len__(self) -> int:
+        return len(self._last)
 
 
 class SwapSpace:
@@ -30,9 +58,9 @@ class SwapSpace:
         # seq_id -> event recorded after its swap-out: its swap-in, on any
         # stream, reads the host pages only after they are written.
         self._swapped_out: Dict[str, torch.cuda.Event] = {}
-        # Recorded after each swap-in: host pages it freed are reused only by
-        # work ordered after it, whichever stream that work runs on.
-        self._swapped_in: Optional[torch.cuda.Event] = None
+        # The event recorded after the swap-in that last read each host page:
+        # a swap-out that reuses the page waits for it, on any stream.
+        self._readers = PageReaders()
         # The reference swaps in from several insertion threads while its
         # engine thread swaps out (paceserve/disutil/decode_instance.py:50-51,
         # paceserve/engine/decode_llm_engine.py:31-41).
@@ -52,15 +80,22 @@ class SwapSpace:
             raise ValueError(f"sequence {seq_id} is already swapped out")
         ids = normalize_page_ids(dev_table, self.dev.num_pages)
         host_table = self.host_allocator.allocate_many(len(ids))
+        stream = torch.cuda.current_stream(self.dev.device)
+        readers = self._readers.take(host_table)
         try:
-            if self._swapped_in is not None:
-                torch.cuda.current_stream(self.dev.device).wait_event(self._swapped_in)
+            for r in readers:
+                stream.wait_event(r)
             ops.swap_out(self.dev, ids, self.host, host_table)
         except Exception:
+            # The pages go back unwritten; an event on this stream, which
+            # already waits for their readers, stands in for those readers.
+            ev = torch.cuda.Event()
+            ev.record(stream)
+            self._readers.record(host_table, ev)
             self.host_allocator.free_many(reversed(host_table))
             raise
         ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(self.dev.device))
+        ev.record(stream)
         self._swapped_out[seq_id] = ev
         self.tables[seq_id] = host_table
         return host_table
@@ -68,8 +103,9 @@ class SwapSpace:
     def swap_in(self, seq_id: str, dev_table: List[int]) -> None:
         """Copies the request's host pages into dev_table (allocated by the
         caller) and returns the host pages to the host allocator.  The copy
-        waits for the request's swap_out, and a later swap_out, on any
-        stream, waits for this copy before it writes host pages."""
+        waits for the request's swap_out, and a later swap_out that reuses any
+        of these host pages, on any stream, waits for this copy before it
+        writes them."""
         with self._lock:
             self._swap_in(seq_id, dev_table)
 
@@ -85,7 +121,7 @@ class SwapSpace:
         ops.swap_in(self.host, host_table, self.dev, ids)
         ev = torch.cuda.Event()
         ev.record(stream)
-        self._swapped_in = ev
+        self._readers.record(host_table, ev)
         del self.tables[seq_id], self._swapped_out[seq_id]
         self.host_allocator.free_many(host_table)
 

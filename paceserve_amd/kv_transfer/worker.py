@@ -12,11 +12,14 @@ and, over a cross-process KVChannel in place of a KVobj returned through
 Ray, _send_kv_cache / _recv_kv_cache with the same free, allocation and
 remap rules.
 
-Two reference defects are not reproduced: the allocate time is reported as
-a positive duration (the reference subtracts the later stamp from the earlier
-one, :280), and when the last logical block has P-1 empty slots the
-reference inserts the same pages twice (:265-277); one insert leaves the same
-bytes.
+The reference's consistency check of the destination table's length
+(:265-266) is kept: an AssertionError with the reference's message.  Three
+reference defects are not reproduced: the allocate time is reported as a
+positive duration (the reference subtracts the later stamp from the earlier
+one, :280); when the last logical block has P-1 empty slots the reference
+inserts the same pages twice (:265-277), where one insert leaves the same
+bytes; and a failed consistency check returns the sequence's destination
+pages before raising, where the reference keeps them allocated.
 """
 from __future__ import annotations
 
@@ -59,14 +62,60 @@ class WorkerSequenceManager:
         return self.block_manager.get_block_table(seq)
 
 
+def check_table_length(seq, n_dst: int, block_len: int) -> None:
+    """The reference's consistency check after allocation
+    (paceserve/worker/base_worker.py:265-266): a sequence that has not been
+    preempted and whose last logical block holds one token (P-1 empty slots)
+    must have received one destination page more than it sent exactly when
+    its prompt fills whole pages (the first generated token then opened a
+    page).  Sequences without the reference's attributes are not checked."""
+    blocks = getattr(seq, "logical_token_blocks", None)
+    state = getattr(seq, "state", None)
+    if not blocks or state is None or not hasattr(seq, "prompt_token_ids"):
+        return
+    P = seq.block_size
+    if blocks[-1].get_num_empty_slots() == P - 1 and getattr(state, "_preemption_count", 0) == 0:
+        want = block_len + (len(seq.prompt_token_ids) % P == 0)
+        assert n_dst == want, f"kv len: {n_dst} block: {block_len} seq: {seq}"
+
+
 class KVWorkerMixin:
     """Provides the worker's KV methods; the host class supplies
     `kvhelper` (a KVhelper), `seq_manager` and `local_rank`."""
 
-    # Inserting threads check for room and allocate as one step (the
-    # reference runs several insertion threads per instance,
-    # paceserve/disutil/decode_instance.py:50).
-    _alloc_lock = threading.Lock()
+    _lock_guard = threading.Lock()
+
+    def _alloc_lock(self, bm):
+        """The lock under which inserting threads check for room and allocate
+        as one step (the reference runs several insertion threads per
+        instance, paceserve/disutil/decode_instance.py:50): the block
+        manager's own, or one per worker for a manager without one."""
+        lock = getattr(bm, "alloc_lock", None)
+        if lock is not None:
+            return lock
+        with KVWorkerMixin._lock_guard:
+            lock = self.__dict__.get("_worker_alloc_lock")
+            if lock is None:
+                lock = self._worker_alloc_lock = threading.Lock()
+        return lock
+
+    def _allocate_dst(self, seq, block_len: int):
+        """Checks for room, allocates the sequence's destination table and
+        applies the reference's length check; returns the table, or None when
+        the destination cannot hold the sequence."""
+        bm = self.seq_manager.block_manager
+        with self._alloc_lock(bm):
+            if bm.get_num_free_gpu_blocks() < bm.get_num_initial_blocks(seq):
+                return None
+            self.seq_manager.add_seq(seq)
+            bm.allocate(seq)
+        kv_indices = self.seq_manager._get_block_table(seq)
+        try:
+            check_table_length(seq, len(kv_indices), block_len)
+        except AssertionError:
+            self.seq_manager._free_seq(seq.seq_id)
+            raise
+        return kv_indices
 
     def _get_kv_cache(self, seq):
         kv_cache, kv_indices = self.kvhelper.get_kv_cache(seq, self.seq_manager)
@@ -81,13 +130,9 @@ class KVWorkerMixin:
         block_len = len(kv_obj.kv_indices)
         cached_content = kv_obj.kv_cache
         allocate_start = time.monotonic()
-        bm = self.seq_manager.block_manager
-        with self._alloc_lock:
-            if bm.get_num_free_gpu_blocks() < bm.get_num_initial_blocks(seq):
-                return False
-            self.seq_manager.add_seq(seq)
-            bm.allocate(seq)
-        kv_indices = self.seq_manager._get_block_table(seq)
+        kv_indices = self._allocate_dst(seq, block_len)
+        if kv_indices is None:
+            return False
         insert_start = time.monotonic()
         # A destination table one page longer than the source (the first
         # generated token opened a page) leaves that last page untouched.
@@ -142,13 +187,9 @@ class KVWorkerMixin:
         payload is then drained by the caller's message())."""
         block_len = len(ref.kv_indices)
         allocate_start = time.monotonic()
-        bm = self.seq_manager.block_manager
-        with self._alloc_lock:
-            if bm.get_num_free_gpu_blocks() < bm.get_num_initial_blocks(seq):
-                return False
-            self.seq_manager.add_seq(seq)
-            bm.allocate(seq)
-        kv_indices = self.seq_manager._get_block_table(seq)
+        kv_indices = self._allocate_dst(seq, block_len)
+        if kv_indices is None:
+            return False
         insert_start = time.monotonic()
         ids = kv_indices if len(kv_indices) == block_len else kv_indices[:-1]
         status = self.kvhelper.recv_kv_cache(channel, ids, device, timeout)

@@ -33,7 +33,7 @@ benchmark and the tests build identical source block tables and pages:
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import List, Optional
+from typing import Iterable, Iterator, List, Optional, Sequence
 
 import numpy as np
 import torch
@@ -85,6 +85,21 @@ class Workload:
     def payload_bytes(self) -> int:
         return self.shape.num_layers * self.n_pages * self.shape.page_bytes
 
+    # The source pool is drawn from `seed`, the destination pool from seed + 50.
+    def src_pool(self, device) -> List[torch.Tensor]:
+        return fill_pool(self.src_pool_pages, self.shape, self.seed, self.init, device)
+
+    def dst_pool(self, device) -> List[torch.Tensor]:
+        return fill_pool(self.dst_pool_pages, self.shape, self.seed + DST_SEED_OFFSET, self.init, device)
+
+    def src_before(self, device) -> Iterator[torch.Tensor]:
+        """src_pool's layers, regenerated one at a time (pool_layers)."""
+        return pool_layers(self.src_pool_pages, self.shape, self.seed, self.init, device)
+
+    def dst_before(self, device) -> Iterator[torch.Tensor]:
+        """dst_pool's layers, regenerated one at a time (pool_layers)."""
+        return pool_layers(self.dst_pool_pages, self.shape, self.seed + DST_SEED_OFFSET, self.init, device)
+
     def summary(self) -> dict:
         return {
             "workload": self.name,
@@ -103,6 +118,7 @@ class Workload:
         }
 
 
+DST_SEED_OFFSET = 50
 LLAMA3_8B = dict(num_layers=32, num_kv_heads=8, head_dim=128, page_size=16)
 
 
@@ -126,11 +142,11 @@ def _lifo_tables(free_list: List[int], lengths: List[int], page_size: int) -> Li
     return tables
 
 
-# The migration workloads, smallest first; the default benchmark workload is
-# the 16-request batch.
+# The migration workloads, smallest first.  The default benchmark workload is
+# the largest one that fits one GPU: 256 requests at the Llama-3-70B KV shape.
 NAMES = ("llama3-8b-512tok-fp16", "llama3-8b-16req-bf16", "llama2-7b-8x4095tok-fp16",
          "llama3-8b-32768tok-bf16", "llama3-70b-256req-bf16")
-DEFAULT = "llama3-8b-16req-bf16"
+DEFAULT = "llama3-70b-256req-bf16"
 PROMOTE = "llama3-8b-4096tok-bf16"
 
 
@@ -202,17 +218,66 @@ def get(name: str) -> Workload:
     raise ValueError(f"unknown workload {name!r} (known: {', '.join(NAMES + (PROMOTE,))})")
 
 
+def _fill_layer(t: torch.Tensor, g: torch.Generator, init: str) -> None:
+    if init == "normal":
+        t.normal_(generator=g)
+    elif init == "uniform4":
+        t.uniform_(-4.0, 4.0, generator=g)
+    else:
+        raise ValueError(init)
+
+
 def fill_pool(layers_pages: int, shape: KVShape, seed: int, init: str, device) -> List[torch.Tensor]:
     """Per-layer pool tensors with seeded values (generated on `device`)."""
     g = torch.Generator(device=device).manual_seed(seed)
     out = []
     for _ in range(shape.num_layers):
         t = torch.empty((layers_pages,) + shape.page_shape, dtype=shape.dtype, device=device)
-        if init == "normal":
-            t.normal_(generator=g)
-        elif init == "uniform4":
-            t.uniform_(-4.0, 4.0, generator=g)
-        else:
-            raise ValueError(init)
+        _fill_layer(t, g, init)
         out.append(t)
     return out
+
+
+def pool_layers(layers_pages: int, shape: KVShape, seed: int, init: str, device) -> Iterator[torch.Tensor]:
+    """The layers fill_pool(layers_pages, shape, seed, init, device) returns,
+    regenerated one at a time into one reused tensor: the same generator
+    draws in the same order give the same values, so a pool's content before
+    a migration can be rebuilt layer by layer without a second pool's memory."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    t = torch.empty((layers_pages,) + shape.page_shape, dtype=shape.dtype, device=device)
+    for _ in range(shape.num_layers):
+        _fill_layer(t, g, init)
+        yield t
+
+
+def migration_mismatch(src_layers: Sequence[torch.Tensor], dst_layers: Sequence[torch.Tensor],
+                       src_ids: torch.Tensor, dst_ids: torch.Tensor,
+                       dst_before: Iterable[torch.Tensor],
+                       src_before: Optional[Iterable[torch.Tensor]] = None) -> Optional[str]:
+    """Exact whole-layer check of a migration, compared as raw bytes.
+
+    For every layer l the destination must equal its content before the
+    migration (dst_before, an iterable of layers; it is modified) with the
+    source's selected pages put in by torch's own indexing,
+        before.index_copy_(0, dst_ids, src_layers[l].index_select(0, src_ids)),
+    which is the reference's gather then scatter (paceserve/kv_transfer/
+    kv_utils.py:44-46,51-52), so a page written twice, swapped, missed or
+    written where no id points fails.  With src_before the source layers must
+    also equal their content before.  Returns None, or a message naming the
+    first layer and the first pages that differ."""
+    si, di = src_ids.long(), dst_ids.long()
+    befores = [dst_before] + ([src_before] if src_before is not None else [])
+    for l, olds in enumerate(zip(*befores)):
+        if l >= len(dst_layers):
+            break
+        want = olds[0]
+        want.index_copy_(0, di, src_layers[l].index_select(0, si))
+        checks = [("destination", dst_layers[l], want)]
+        if src_before is not None:
+            checks.append(("source", src_layers[l], olds[1]))
+        for what, got, exp in checks:
+            a, b = got.view(torch.uint8), exp.view(torch.uint8)
+            if not torch.equal(a, b):
+                bad = (a != b).reshape(a.shape[0], -1).any(1).nonzero().flatten()[:4].tolist()
+                return f"layer {l}: {what} pages {bad} differ"
+    return None

@@ -219,7 +219,8 @@ def test_worker_send_and_receive(gpu, tokens_src, tokens_dst):
     src_w.seq_manager.block_manager.allocate(seq)
     src_table = src_w.seq_manager._get_block_table(seq)
     free_before = src_w.seq_manager.block_manager.get_num_free_gpu_blocks()
-    dst_seq = Sequence.of_length("r", tokens_dst, P)
+    # the decode side's sequence holds the prompt and the first generated token(s)
+    dst_seq = Sequence.of_length("r", tokens_src, P, tokens_dst - tokens_src)
     before = [words(c).clone() for c in dst_cache]
     got = {}
 

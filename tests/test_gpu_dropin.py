@@ -183,7 +183,8 @@ def test_worker_migration_end_to_end(gpu, tokens_src, tokens_dst):
     assert kv_indices == src_table and rank == 0
     assert src_sm.block_manager.get_num_free_gpu_blocks() == free_before + len(src_table)
     obj = KVobj(seq.seq_id, kv_cache, kv_indices)
-    dst_seq = Sequence.of_length("r", tokens_dst, P)
+    # the decode side's sequence holds the prompt and the first generated token(s)
+    dst_seq = Sequence.of_length("r", tokens_src, P, tokens_dst - tokens_src)
     dst_before = [words(c).clone() for c in dst_cache]
     st = dst_w._insert_kv_cache(dst_seq, obj, gpu)
     assert isinstance(st, KVStatus) and st.status

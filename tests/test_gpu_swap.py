@@ -196,10 +196,48 @@ def test_swap_space_orders_work_across_streams(gpu):
 
 def test_swap_4k_request(gpu):
     w = workloads.get(workloads.PROMOTE)
-    dev = ops.PagedPool(workloads.fill_pool(w.src_pool_pages, w.shape, w.seed, w.init, gpu))
+    dev = ops.PagedPool(w.src_pool(gpu))
     host = ops.HostPagePool.like(dev, 256)
     ids = w.src_tables[0]
     ops.swap_out(dev, ids, host, list(range(256)))
     torch.cuda.synchronize()
     for l in (0, 13, 31):
         assert torch.equal(words(host.layers[l]), words(dev.layers[l][torch.tensor(ids, device=gpu)].cpu()))
+
+
+def test_swap_space_waits_for_every_swap_in_that_read_reused_pages(gpu):
+    # Two requests swap in on two streams, the first held back behind long
+    # device copies; a third request then swaps out on a third stream into
+    # host pages that both swap-ins read.  Its writes must wait for both
+    # readers, not only for the swap-in enqueued last.
+    dev = dev_pool(gpu, 1280, 11)
+    alloc = NativeBlockAllocator(16, 1280)
+    space = SwapSpace(dev, 400)
+    ids = lambda t: torch.tensor(t, device=gpu)           # noqa: E731
+    t1, t2, t3 = alloc.allocate_many(200), alloc.allocate_many(200), alloc.allocate_many(400)
+    saved = {k: [words(t[ids(tab)]).clone() for t in dev.layers] for k, tab in (("r1", t1), ("r2", t2), ("r3", t3))}
+    space.swap_out("r1", t1)
+    space.swap_out("r2", t2)
+    new1, new2 = alloc.allocate_many(200), alloc.allocate_many(200)
+    x = torch.empty(4 << 30, dtype=torch.uint8, device=gpu).fill_(1)
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    a, b, c = torch.cuda.Stream(gpu), torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)
+    with torch.cuda.stream(a):
+        for _ in range(8):                 # ~15 ms of copies ahead of r1's swap-in
+            y.copy_(x)
+        space.swap_in("r1", new1)
+    with torch.cuda.stream(b):
+        space.swap_in("r2", new2)
+    with torch.cuda.stream(c):
+        space.swap_out("r3", t3)           # all 400 host pages: r1's and r2's
+    torch.cuda.synchronize()
+    for l in range(SHAPE.num_layers):
+        assert torch.equal(words(dev.layers[l][ids(new1)]), saved["r1"][l]), f"r1 layer {l}"
+        assert torch.equal(words(dev.layers[l][ids(new2)]), saved["r2"][l]), f"r2 layer {l}"
+    alloc.free_many(new1 + new2)
+    new3 = alloc.allocate_many(400)
+    space.swap_in("r3", new3)
+    torch.cuda.synchronize()
+    for l in range(SHAPE.num_layers):
+        assert torch.equal(words(dev.layers[l][ids(new3)]), saved["r3"][l]), f"r3 layer {l}"

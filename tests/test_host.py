@@ -177,19 +177,52 @@ class _Content:
         return 2 * self.shape[1]
 
 
-@pytest.mark.parametrize("tokens,src_pages,expect_ids", [
-    (40, 3, [9, 8, 7]),          # n pages on both sides
-    (49, 3, [9, 8, 7]),          # destination has n+1: last page untouched
+@pytest.mark.parametrize("prompt,outputs,src_pages,expect_ids", [
+    (40, 0, 3, [9, 8, 7]),       # n pages on both sides
+    (48, 1, 3, [9, 8, 7]),       # the first generated token opened page n+1: it stays untouched
+    (40, 1, 3, [9, 8, 7]),
 ])
-def test_worker_insert_remaps_like_reference(tokens, src_pages, expect_ids):
+def test_worker_insert_remaps_like_reference(prompt, outputs, src_pages, expect_ids):
     helper = _FakeHelper()
     worker = KVWorker(helper, WorkerSequenceManager(16, 10))
-    seq = Sequence.of_length("r", tokens, 16)
+    seq = Sequence.of_length("r", prompt, 16, outputs)
     kv = KVobj("r", _Content(src_pages), list(range(src_pages)))
     st = worker._insert_kv_cache(seq, kv, "cuda:0")
     assert isinstance(st, KVStatus) and st.status
     assert helper.calls == [expect_ids]
     assert st.allocate_time >= 0 and st.insertion_time >= 0
+
+
+def test_worker_insert_checks_table_length_like_reference():
+    """base_worker.py:265-266: a sequence whose last block holds one token and
+    whose prompt does not fill whole pages must not get an extra page; the
+    check raises the reference's AssertionError, and the pages go back."""
+    helper = _FakeHelper()
+    worker = KVWorker(helper, WorkerSequenceManager(16, 10))
+    seq = Sequence.of_length("r", 49, 16)        # 49 prompt tokens: 4 pages, the last with 15 empty slots
+    with pytest.raises(AssertionError, match="kv len: 4 block: 3 seq: "):
+        worker._insert_kv_cache(seq, KVobj("r", _Content(3), [0, 1, 2]), 0)
+    assert helper.calls == []
+    assert worker.seq_manager.block_manager.get_num_free_gpu_blocks() == 10
+    assert "r" not in worker.seq_manager.seq_map
+    # a preempted sequence is not checked (its table may be a page longer)
+    seq.state._preemption_count = 1
+    st = worker._insert_kv_cache(seq, KVobj("r", _Content(3), [0, 1, 2]), 0)
+    assert st.status and helper.calls == [[6, 7, 8]]      # the returned pages come back LIFO
+
+
+def test_worker_alloc_lock_is_per_block_manager():
+    a = KVWorker(_FakeHelper(), WorkerSequenceManager(16, 10))
+    b = KVWorker(_FakeHelper(), WorkerSequenceManager(16, 10))
+    la = a._alloc_lock(a.seq_manager.block_manager)
+    assert la is a.seq_manager.block_manager.alloc_lock
+    assert la is not b._alloc_lock(b.seq_manager.block_manager)
+
+    class Bare:                                 # a manager without a lock of its own
+        pass
+
+    assert a._alloc_lock(Bare()) is a._alloc_lock(Bare())
+    assert a._alloc_lock(Bare()) is not b._alloc_lock(Bare())
 
 
 def test_worker_insert_without_room_returns_false():
@@ -217,3 +250,33 @@ def test_kvobj_size_in_megabytes():
     import torch
     t = torch.zeros(2, 3, 2, 16, 8, 128, dtype=torch.float16)
     assert KVobj("x", t, [0, 1, 2]).size == t.numel() * 2 / 1e6
+
+
+def test_page_readers_return_each_reader_of_reused_pages_once():
+    from paceserve_amd.kv_transfer.swap import PageReaders
+
+    r = PageReaders()
+    r.record([5, 6, 7], "swap_in_A")          # stream S1
+    r.record([1, 2], "swap_in_B")             # stream S2, enqueued later
+    # a swap-out reusing pages of both swap-ins waits for both, once each
+    assert r.take([2, 7, 1, 6, 9]) == ["swap_in_B", "swap_in_A"]
+    assert len(r) == 1                        # page 5 still remembers A
+    assert r.take([5]) == ["swap_in_A"] and r.take([5]) == []
+    # a later reader of a page replaces the earlier one
+    r.record([3], "A")
+    r.record([3], "C")
+    assert r.take([3]) == ["C"]
+
+
+def test_host_destination_ids_must_be_distinct():
+    """Repeated destination ids given as host data are refused before any
+    copy (two waves writing one page race); source ids may repeat."""
+    import torch
+
+    from paceserve_amd.kv_transfer import ops
+
+    with pytest.raises(ValueError, match="destination page 3 appears more than once"):
+        ops.device_ids([5, 3, 1, 3], torch.device("cpu"), distinct=True)
+    with pytest.raises(ValueError, match="destination page 7 appears"):
+        ops.device_ids(torch.tensor([7, 7]), torch.device("cpu"), distinct=True)
+    assert ops.device_ids([], torch.device("cpu"), distinct=True).numel() == 0
