@@ -195,6 +195,32 @@ int pace_kv_unpack_from_host(pace_kv_stager* stager, const void* host_in,
                              int layers_per_chunk, int32_t* err_count,
                              void* stream);
 
+/* Bytes of the device scratch array through which
+ * pace_kv_pack_to_host_noalloc stages its chunks (64 MiB per GPU). */
+#define PACE_KV_NOALLOC_SCRATCH_BYTES (64 << 20)
+
+/*
+ * Allocation-free pack into host memory.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc), which
+ * cannot create a pace_kv_stager.  It writes the same host_out bytes as
+ * pace_kv_pack_to_host, with no stager: each chunk is packed into a device
+ * scratch array of PACE_KV_NOALLOC_SCRATCH_BYTES, which the library holds on
+ * every GPU it runs on until the process ends, and copied from there to
+ * host_out, pack and copy both on `stream` (no side stream, so a chunk's pack
+ * does not overlap the previous chunk's copy).  Chunks are whole layers when
+ * one layer's n_pages * page_bytes fits the scratch, else runs of pages of
+ * one layer; a page larger than the scratch is rejected (PACE_KV_ERANGE).
+ * It calls no hipMalloc or hipFree.  Every call on one GPU shares that GPU's
+ * scratch: calls on one stream from one host thread are ordered, while calls
+ * that overlap (on several streams, or from several host threads) race on it.
+ */
+int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers,
+                                 int64_t pool_pages, const int32_t* page_ids,
+                                 int64_t n_pages, int64_t page_bytes,
+                                 void* host_out, int32_t* err_count,
+                                 void* stream);
+
 /*
  * Full host round trip in one pipeline: pack(c) -> D2H(c) -> H2D(c) ->
  * unpack(c) per layer chunk, with pack(c+1), D2H(c), H2D(c-1) and

@@ -21,12 +21,47 @@
 // that slot, so back-to-back calls on one stager are ordered correctly.
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "internal.h"
 
 using pace_kv::fail;
 using pace_kv::hip_status;
+
+// Device staging of pace_kv_pack_to_host_noalloc: one array per GPU, which
+// the runtime places when it loads this code object on that GPU and which
+// stays until the process ends.  Host code never uses this name as an
+// address (on the host it is a stand-in): the device address comes from
+// hipGetSymbolAddress, once per device, and is kept in g_scratch.
+static __device__ __align__(256) char scratch[PACE_KV_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch[kMaxDevices];  // device address of `scratch` on each device, once looked up
+
+// The address of the current device's scratch array, looked up on the first
+// call on that device.
+int current_scratch(char** out) {
+  int dev = -1;
+  PACE_KV_TRY(hip_status(hipGetDevice(&dev), "hipGetDevice"));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(PACE_KV_ESTATE, "device %d is outside the %d devices the scratch table covers", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    PACE_KV_TRY(hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"));
+    if (p == nullptr) return fail(PACE_KV_ESTATE, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch[dev] = static_cast<char*>(p);
+  }
+  *out = g_scratch[dev];
+  return PACE_KV_OK;
+}
+
+}  // namespace
 
 struct pace_kv_stager {
   int device = -1;
@@ -305,6 +340,54 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
   // The caller's later work sees every destination page written.
   PACE_HIP(hipEventRecord(s->unpack_done, s->unpack), "record unpack_done");
   PACE_HIP(hipStreamWaitEvent(stream, s->unpack_done, 0), "join unpacks");
+  return PACE_KV_OK;
+}
+
+int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers, int64_t pool_pages,
+                                 const int32_t* page_ids, int64_t n_pages, int64_t page_bytes,
+                                 void* host_out, int32_t* err_count, void* stream_) {
+  const int64_t cap = PACE_KV_NOALLOC_SCRATCH_BYTES;
+  if (num_layers < 0 || n_pages < 0) return fail(PACE_KV_EINVAL, "negative num_layers or n_pages");
+  if (page_bytes <= 0 || page_bytes % 16 != 0)
+    return fail(PACE_KV_EINVAL, "page_bytes must be a positive multiple of 16");
+  if (page_bytes > cap)
+    return fail(PACE_KV_ERANGE, "pack_to_host_noalloc: a page of %lld bytes exceeds the %lld-byte scratch",
+                (long long)page_bytes, (long long)cap);
+  if (n_pages > INT64_MAX / page_bytes) return fail(PACE_KV_ERANGE, "payload size overflows");
+  if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
+  if (host_out == nullptr) return fail(PACE_KV_EINVAL, "pack_to_host_noalloc: host_out is NULL");
+  char* slot = nullptr;
+  PACE_KV_TRY(current_scratch(&slot));
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  char* host = static_cast<char*>(host_out);
+  const int64_t layer_bytes = n_pages * page_bytes;
+  // Every pack and copy runs on `stream`, so a chunk's pack overwrites the
+  // scratch only after the previous chunk's copy has read it.
+  if (layer_bytes <= cap) {
+    // chunks of whole layers
+    const int64_t k64 = cap / layer_bytes;
+    const int k = k64 < num_layers ? static_cast<int>(k64) : num_layers;
+    for (int l0 = 0; l0 < num_layers; l0 += k) {
+      const int nl = num_layers - l0 < k ? num_layers - l0 : k;
+      PACE_KV_TRY(pace_kv_pack(src_layers + l0, nl, pool_pages, page_ids, n_pages, page_bytes, slot,
+                               layer_bytes, err_count, stream));
+      PACE_HIP(hipMemcpyAsync(host + l0 * layer_bytes, slot, nl * layer_bytes, hipMemcpyDeviceToHost, stream),
+               "D2H copy");
+    }
+  } else {
+    // runs of pages of one layer
+    const int64_t run = cap / page_bytes;
+    for (int l = 0; l < num_layers; ++l) {
+      for (int64_t p0 = 0; p0 < n_pages; p0 += run) {
+        const int64_t np = n_pages - p0 < run ? n_pages - p0 : run;
+        PACE_KV_TRY(pace_kv_pack(src_layers + l, 1, pool_pages, page_ids + p0, np, page_bytes, slot,
+                                 np * page_bytes, err_count, stream));
+        PACE_HIP(hipMemcpyAsync(host + l * layer_bytes + p0 * page_bytes, slot, np * page_bytes,
+                                hipMemcpyDeviceToHost, stream),
+                 "D2H copy");
+      }
+    }
+  }
   return PACE_KV_OK;
 }
 

@@ -106,3 +106,17 @@ def test_header_is_self_contained_c_and_cpp(tmp_path, compiler, flags):
     r = subprocess.run([compiler, *flags, "-Wall", "-Wextra", "-Werror", "-pedantic", f"-I{HEADER.parent}",
                         "-fsyntax-only", str(src)], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_noalloc_pack_to_host_rejects_pages_beyond_its_scratch(lib):
+    """A page larger than the 64 MiB scratch is refused before any device
+    call (so this runs without a GPU), with the limit in the message."""
+    big = _native.NOALLOC_SCRATCH_BYTES + 16
+    rc = lib.pace_kv_pack_to_host_noalloc(_layers(1), 1, 4, 0x100, 1, big, 0x1000, None, None)
+    assert rc == _native.PACE_KV_ERANGE
+    assert b"exceeds the 67108864-byte scratch" in lib.pace_kv_last_error()
+    assert lib.pace_kv_pack_to_host_noalloc(_layers(1), 1, 4, 0x100, 1, 24, 0x1000, None, None) == \
+        _native.PACE_KV_EINVAL                                      # not a multiple of 16
+    assert lib.pace_kv_pack_to_host_noalloc(None, 0, 4, None, 3, 65536, None, None, None) == 0   # no work
+    text = HEADER.read_text()
+    assert "#define PACE_KV_NOALLOC_SCRATCH_BYTES (64 << 20)" in text
