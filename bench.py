@@ -526,12 +526,16 @@ def run_dropin(dev, steps: int = 10, warmup: int = 2) -> dict:
 CHANNEL_SLOT_BYTES = 32 << 20
 CHANNEL_SLOTS = 4
 CHANNEL_THREADS = 4
+# The same-GPU device ring: 4 slots of 128 MiB (one 512 MiB allocation shared
+# between the two processes).
+CHANNEL_DEVICE_SLOT_BYTES = 128 << 20
 
 
 def channel_sender(name: str) -> None:
     """The sending process of the channel leg: builds the 4096-token
     request's source pool (seeded, on the GPU) and sends the request once per
-    line read from stdin, as a prefill instance answers each pull."""
+    line read from stdin, as a prefill instance answers each pull.  On the
+    GPU of a channel's device ring the pages go through that ring."""
     import torch
 
     from paceserve_amd import _native, workloads
@@ -549,37 +553,23 @@ def channel_sender(name: str) -> None:
             ch.send(src, ids, line.strip().encode(), timeout=120)
 
 
-def run_channel(dev, runs: int = 10, warmup: int = 2, ref_runs: int = 3) -> dict:
-    """The 4096-token request moved from another process's cache into this
-    one's through the shared-memory channel: this process asks (a line on the
-    sender's stdin, as a decode instance pulls a sequence), receives the
-    header and unpacks the pages; wall-clock from the ask to the last unpack.
-    Beside it, the reference's path for the same hop, run in this process on
-    a copy of the source pool: get_kv_cache into a pageable tensor
-    (paceserve/kv_transfer/kv_utils.py:44-46), a pickle round trip standing in
-    for the object store (prefill_instance.py:96-107, decode_instance.py:
-    165-171; Ray's RPCs and inter-process copies are left out, so this
-    understates its cost), and insert_kv_cache (:51-52)."""
-    import pickle
+def channel_leg(dev, w, dst, d_ids, device_slot_bytes: int, runs: int, warmup: int) -> dict:
+    """Moves the request `warmup + runs` times from a sender process into
+    `dst` through one channel (device_slot_bytes > 0: with a device ring);
+    wall-clock from the ask (a line on the sender's stdin) to the last unpack."""
     import subprocess
 
     import torch
 
-    from paceserve_amd import workloads
-    from paceserve_amd.kv_transfer import ops
     from paceserve_amd.kv_transfer.channel import KVChannel
 
-    w = workloads.get(workloads.PROMOTE)
-    L, n = w.shape.num_layers, w.n_pages
-    ids = list(w.src_tables[0])
-    dst_ids = list(range(w.dst_pool_pages - 1, w.dst_pool_pages - 1 - n, -1))
-    name = f"pace_bench_{os.getpid()}"
-    ch = KVChannel.create(name, CHANNEL_SLOT_BYTES, CHANNEL_SLOTS, CHANNEL_THREADS)
+    n = w.n_pages
+    name = f"pace_bench_{os.getpid()}_{device_slot_bytes}"
+    ch = KVChannel.create(name, CHANNEL_SLOT_BYTES, CHANNEL_SLOTS, CHANNEL_THREADS,
+                          device_slot_bytes=device_slot_bytes)
     child = subprocess.Popen([sys.executable, str(ROOT / "bench.py"), "--channel-sender", name],
                              stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True)
     try:
-        dst = ops.PagedPool(w.dst_pool(dev))
-        d_ids = ops.device_ids(dst_ids, dev)
         if child.stdout.readline().strip() != "ready":
             raise RuntimeError("channel sender did not start")
         ts = []
@@ -602,16 +592,55 @@ def run_channel(dev, runs: int = 10, warmup: int = 2, ref_runs: int = 3) -> dict
         if child.poll() is None:
             child.kill()
         ch.close()
+    ts.sort()
     ms = statistics.median(ts) * 1e3
+    return {"ms": round(ms, 3), "gbs": round(w.payload_bytes / (ms / 1e3) / 1e9, 2),
+            "p90_ms": round(ts[int(0.9 * (len(ts) - 1))] * 1e3, 3), "runs": runs}
+
+
+def run_channel(dev, runs: int = 10, warmup: int = 2, ref_runs: int = 3) -> dict:
+    """The 4096-token request moved from another process's cache into this
+    one's through the channel: this process asks (a line on the sender's
+    stdin, as a decode instance pulls a sequence), receives the header and
+    unpacks the pages; wall-clock from the ask to the last unpack.  Two
+    channels: one with a same-GPU device ring (the pages never leave HBM) and
+    one through the shared-memory ring only (what two processes on different
+    GPUs, or a host payload, use).  Beside them, the reference's path for the
+    same hop, run in this process on a copy of the source pool: get_kv_cache
+    into a pageable tensor (paceserve/kv_transfer/kv_utils.py:44-46), a pickle
+    round trip standing in for the object store (prefill_instance.py:96-107,
+    decode_instance.py:165-171; Ray's RPCs and inter-process copies are left
+    out, so this understates its cost), and insert_kv_cache (:51-52)."""
+    import pickle
+
+    import torch
+
+    from paceserve_amd import workloads
+    from paceserve_amd.kv_transfer import ops
+
+    w = workloads.get(workloads.PROMOTE)
+    L, n = w.shape.num_layers, w.n_pages
+    ids = list(w.src_tables[0])
+    dst_ids = list(range(w.dst_pool_pages - 1, w.dst_pool_pages - 1 - n, -1))
     src = w.src_pool(dev)
     si, di = torch.tensor(ids, device=dev), torch.tensor(dst_ids, device=dev)
-    ok = all(torch.equal(d[di].view(torch.int16), s[si].view(torch.int16)) for d, s in zip(dst.layers, src))
     out = {"payload_bytes": w.payload_bytes, "workload": w.name, "runs": runs,
            "slot_bytes": CHANNEL_SLOT_BYTES, "slots": CHANNEL_SLOTS, "copy_threads_per_side": CHANNEL_THREADS,
-           "channel_ms": round(ms, 2), "channel_gbs": round(w.payload_bytes / (ms / 1e3) / 1e9, 2),
-           "channel_p90_ms": round(sorted(ts)[int(0.9 * (len(ts) - 1))] * 1e3, 2), "same_bytes": ok}
-    log(f"channel: {ms:.2f} ms per request across processes, {out['channel_gbs']} GB/s, same bytes {ok}")
-    del dst
+           "device_slot_bytes": CHANNEL_DEVICE_SLOT_BYTES}
+    for label, dsb in (("device_ring", CHANNEL_DEVICE_SLOT_BYTES), ("shm_ring", 0)):
+        dst = ops.PagedPool(w.dst_pool(dev))
+        d_ids = ops.device_ids(dst_ids, dev)
+        leg = channel_leg(dev, w, dst, d_ids, dsb, runs, warmup)
+        leg["same_bytes"] = all(torch.equal(d[di].view(torch.int16), s[si].view(torch.int16))
+                                for d, s in zip(dst.layers, src))
+        out[label] = leg
+        log(f"channel {label}: {leg['ms']} ms per request across processes, {leg['gbs']} GB/s, "
+            f"same bytes {leg['same_bytes']}")
+        del dst
+    # the headline figures: the same-GPU device ring
+    out["channel_ms"] = out["device_ring"]["ms"]
+    out["channel_gbs"] = out["device_ring"]["gbs"]
+    out["same_bytes"] = out["device_ring"]["same_bytes"] and out["shm_ring"]["same_bytes"]
     dst = w.dst_pool(dev)
     rts = []
     for r in range(1 + ref_runs):
@@ -631,7 +660,7 @@ def run_channel(dev, runs: int = 10, warmup: int = 2, ref_runs: int = 3) -> dict
     out["reference_emulated_gbs"] = round(w.payload_bytes / (rms / 1e3) / 1e9, 2)
     out["reference_emulated"] = ("get_kv_cache (pageable, per layer) + pickle.dumps/loads + insert_kv_cache "
                                  "(per layer), one process; excludes Ray's RPCs and object-store copies")
-    out["speedup_vs_reference_emulated"] = round(rms / ms, 2)
+    out["speedup_vs_reference_emulated"] = round(rms / out["channel_ms"], 2)
     log(f"channel reference path (emulated): {rms:.2f} ms")
     return out
 

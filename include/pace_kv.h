@@ -407,6 +407,26 @@ typedef struct pace_kv_channel pace_kv_channel;
  * creator's close unlinks the name.  copy_threads in [1, 64]. */
 int pace_kv_channel_create(const char* name, int64_t slot_bytes, int num_slots,
                            int copy_threads, pace_kv_channel** out);
+/* As pace_kv_channel_create, plus a device ring on the current GPU for peers
+ * on the same GPU: num_slots device slots of dev_slot_bytes (a multiple of
+ * 4096; num_slots * dev_slot_bytes at most 1 GiB), allocated here and
+ * exported with hipIpcGetMemHandle.  A pace_kv_channel_send made on that GPU
+ * packs each chunk straight into a device slot (chunks sized to
+ * dev_slot_bytes), and the receiving endpoint unpacks straight out of it, so
+ * the payload never leaves HBM; the other endpoint opens the ring on its
+ * first device transfer.  Sends from another GPU, and send_host, use the
+ * shared-memory slots as before.  Replaces, for two instance processes on one
+ * GPU, the same object-store hop as pace_kv_channel_create
+ * (paceserve/disutil/prefill_instance.py:96-107,
+ *  paceserve/disutil/decode_instance.py:165-171). */
+int pace_kv_channel_create_device(const char* name, int64_t slot_bytes,
+                                  int num_slots, int copy_threads,
+                                  int64_t dev_slot_bytes,
+                                  pace_kv_channel** out);
+/* The device ring's slot bytes (0: the channel has none) and whether it lives
+ * on the current GPU (sends from this GPU then use it). */
+int pace_kv_channel_device_info(pace_kv_channel* channel,
+                                int64_t* dev_slot_bytes, int* on_current_gpu);
 /* Opens a channel created by the peer, waiting up to timeout_ms for it. */
 int pace_kv_channel_open(const char* name, int copy_threads, int timeout_ms,
                          pace_kv_channel** out);
@@ -423,7 +443,8 @@ int pace_kv_channel_unlink(const char* name);
 /* Sends one message whose payload is packed from device pools:
  *   payload[l][j] = src_layers[l][page_ids[j]] (page_ids: device int32).
  * Packs run on `stream` after its earlier work.  Returns once every chunk is
- * in the ring (host-synchronous); *msg_id receives the message's id. */
+ * in the ring (host-synchronous); *msg_id receives the message's id.  On the
+ * GPU of a channel's device ring the chunks go into device slots. */
 int pace_kv_channel_send(pace_kv_channel* channel,
                          const void* const* src_layers, int num_layers,
                          int64_t pool_pages, const int32_t* page_ids,
@@ -452,7 +473,8 @@ int pace_kv_channel_recv_header(pace_kv_channel* channel, void* meta,
  *   dst_layers[l][page_ids[j]] = payload[l][j] (page_ids: device int32,
  * distinct).  The shape must equal the header's.  Unpacks run on `stream`
  * after its earlier work; the call returns once every chunk has left the
- * ring, with the last unpacks still enqueued.  Ids outside [0, pool_pages)
+ * ring, with the last unpacks still enqueued (a payload in device slots:
+ * with every unpack finished, since a slot is released only then).  Ids outside [0, pool_pages)
  * are skipped and counted in err_count, as in pace_kv_unpack.  After a
  * PACE_KV_ETIMEDOUT the call may be repeated and continues where it
  * stopped. */

@@ -63,6 +63,8 @@ SIGNATURES = {
         [_VP, _VP, _VP, c_int64, _VP, c_int64, c_int, c_int64, c_int, _VP, _VP, _VP, _VP, c_int64,
          c_int, _VP, _VP, _VP]),
     "pace_kv_channel_create": (c_int, [c_char_p, c_int64, c_int, c_int, POINTER(c_void_p)]),
+    "pace_kv_channel_create_device": (c_int, [c_char_p, c_int64, c_int, c_int, c_int64, POINTER(c_void_p)]),
+    "pace_kv_channel_device_info": (c_int, [_VP, POINTER(c_int64), POINTER(c_int)]),
     "pace_kv_channel_open": (c_int, [c_char_p, c_int, c_int, POINTER(c_void_p)]),
     "pace_kv_channel_close": (c_int, [_VP]),
     "pace_kv_channel_info": (c_int, [_VP, POINTER(c_int64), POINTER(c_int)]),

@@ -23,6 +23,15 @@
 // copies a shared slot into a pinned slot (releasing the shared slot at once),
 // then uploads it and unpacks it while the next chunk is copied.
 //
+// Same-GPU device ring: a creator may also allocate a ring of device slots
+// (pace_kv_channel_create_device) and export it with hipIpcGetMemHandle; the
+// other process opens the handle on its first device transfer.  A device
+// send then packs each chunk straight into a device slot and publishes it
+// once its pack has finished; the receiver unpacks from that slot and
+// releases it once its unpack has finished.  Those payload bytes never leave
+// HBM.  Headers still travel in the shared-memory slots, and a message is
+// wholly in device slots or wholly in host slots (the header says which).
+//
 // Failures: every wait has a deadline and ends when either side closes the
 // channel; the control block records which process plays each role, so a
 // wait also ends when the peer process has exited.  A sender that fails
@@ -44,6 +53,7 @@
 #include <atomic>
 #include <chrono>
 #include <condition_variable>
+#include <map>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -57,11 +67,17 @@ using pace_kv::hip_status;
 namespace {
 
 constexpr uint64_t kMagic = 0x50414345'4b564348ull;  // "PACEKVCH"
-constexpr uint32_t kVersion = 2;
+constexpr uint32_t kVersion = 3;
 constexpr int kMaxSlots = 64;
 constexpr int kNameMax = 200;
+// Largest device ring: one shared allocation, kept well under the 2 GiB
+// beyond which opening an exported allocation was seen not to return.
+constexpr int64_t kMaxDeviceRing = int64_t(1) << 30;
+constexpr int kBusIdBytes = 64;
 
-enum RecordKind : uint32_t { kEmpty = 0, kHeader = 1, kData = 2 };
+enum RecordKind : uint32_t { kEmpty = 0, kHeader = 1, kData = 2, kDevData = 3 };
+// Header flags.
+constexpr int32_t kDevicePayload = 1;  // the payload's chunks are in device slots
 
 static_assert(sizeof(std::atomic<uint32_t>) == 4, "futex words are 32-bit");
 static_assert(std::atomic<uint32_t>::is_always_lock_free, "shared counters must be lock-free");
@@ -76,7 +92,7 @@ struct alignas(64) SlotRecord {
   int64_t n_pages;       // header
   int64_t page_bytes;    // header
   int32_t num_layers;    // header
-  int32_t pad;
+  int32_t flags;         // header: kDevicePayload
 };
 
 // Which process plays a role (sender or receiver): its pid, its pid
@@ -102,6 +118,14 @@ struct alignas(64) ChannelCtl {
   std::atomic<uint64_t> aborted_msg;         // sender: id of a message it gave up (0 = none)
   ProcessId sender, receiver;
   SlotRecord slots[kMaxSlots];
+  // Device ring (dev_slot_bytes 0: none): num_slots device slots of
+  // dev_slot_bytes, allocated by the process dev_owner_pid on the GPU
+  // dev_bus_id, exported as dev_handle.
+  int64_t dev_slot_bytes;
+  int32_t dev_owner_pid;
+  int32_t dev_pad;
+  char dev_bus_id[kBusIdBytes];
+  hipIpcMemHandle_t dev_handle;
 };
 
 // head and tail count records modulo 2^32 and a record's slot is the count
@@ -362,9 +386,17 @@ struct pace_kv_channel {
   Staging tx, rx;       // device staging of sends and of receives
   // receiver state of the message in progress
   bool rx_active = false;
+  bool rx_device = false;  // its payload is in device slots
   uint64_t rx_msg = 0;
   Chunking rx_chunks;
   int64_t rx_next = 0;
+  // this process's view of the device ring
+  char* dev_ring = nullptr;
+  int dev_device = -1;
+  bool dev_allocated = false;  // hipMalloc'ed here (freed at close)
+  bool dev_imported = false;   // opened from the exported handle (closed at close)
+  std::vector<hipEvent_t> dev_packed;    // sender: pack into slot i finished
+  std::vector<hipEvent_t> dev_unpacked;  // receiver: unpack out of slot i finished
 };
 
 namespace {
@@ -478,7 +510,42 @@ void free_staging(Staging& s) {
   s = Staging();
 }
 
+// Process-local registry of the device rings this process allocated, by the
+// inode of their channel's shared-memory object: an endpoint that opens a
+// channel created in its own process uses the ring's address directly, since
+// an exported handle is not opened in the process that exported it.
+std::mutex g_rings_mu;
+std::map<uint64_t, char*> g_rings;
+
+uint64_t shm_inode(int fd) {
+  struct stat st;
+  return fd >= 0 && fstat(fd, &st) == 0 ? static_cast<uint64_t>(st.st_ino) : 0;
+}
+
+void free_device_ring(pace_kv_channel* ch) {
+  for (std::vector<hipEvent_t>* v : {&ch->dev_packed, &ch->dev_unpacked}) {
+    for (hipEvent_t e : *v) {
+      (void)hipEventSynchronize(e);
+      (void)hipEventDestroy(e);
+    }
+    v->clear();
+  }
+  if (ch->dev_ring != nullptr) {
+    if (ch->dev_imported) (void)hipIpcCloseMemHandle(ch->dev_ring);
+    if (ch->dev_allocated) {
+      {
+        std::lock_guard<std::mutex> lock(g_rings_mu);
+        g_rings.erase(shm_inode(ch->fd));
+      }
+      (void)hipFree(ch->dev_ring);
+    }
+  }
+  ch->dev_ring = nullptr;
+  ch->dev_imported = ch->dev_allocated = false;
+}
+
 void destroy(pace_kv_channel* ch) {
+  free_device_ring(ch);
   free_staging(ch->tx);
   free_staging(ch->rx);
   delete ch->pool;
@@ -541,7 +608,7 @@ int staging_ready(pace_kv_channel* ch, Staging& s) {
 
 // Publishes the header record of a new message; returns its id.
 int send_header(pace_kv_channel* ch, int num_layers, int64_t n_pages, int64_t page_bytes, const void* meta,
-                int64_t meta_bytes, int timeout_ms, uint64_t* msg_id) {
+                int64_t meta_bytes, int timeout_ms, uint64_t* msg_id, int32_t flags = 0) {
   ChannelCtl* c = ch->ctl;
   take_role(c->sender);
   if (meta_bytes < 0 || (meta_bytes > 0 && meta == nullptr))
@@ -562,6 +629,7 @@ int send_header(pace_kv_channel* ch, int num_layers, int64_t n_pages, int64_t pa
   r.n_pages = n_pages;
   r.page_bytes = page_bytes;
   r.num_layers = num_layers;
+  r.flags = flags;
   publish(ch);
   if (msg_id) *msg_id = id;
   return PACE_KV_OK;
@@ -608,7 +676,8 @@ int next_chunk(pace_kv_channel* ch, int timeout_ms, uint32_t* idx, Chunking::Chu
   PACE_KV_TRY(next_record(ch, timeout_ms, idx, "a payload chunk"));
   const SlotRecord& r = ch->ctl->slots[*idx];
   *k = ch->rx_chunks.at(ch->rx_next);
-  if (r.kind != kData || r.msg_id != ch->rx_msg || r.chunk != static_cast<uint32_t>(ch->rx_next) ||
+  const uint32_t kind = ch->rx_device ? kDevData : kData;
+  if (r.kind != kind || r.msg_id != ch->rx_msg || r.chunk != static_cast<uint32_t>(ch->rx_next) ||
       r.offset != k->offset || r.bytes != k->bytes) {
     ch->rx_active = false;
     return fail(PACE_KV_ESTATE, "channel %s: expected chunk %lld of message %llu, found a record of "
@@ -623,12 +692,172 @@ void finish_chunk(pace_kv_channel* ch) {
   if (++ch->rx_next == ch->rx_chunks.num_chunks) ch->rx_active = false;
 }
 
+// ------------------------------------------------------------ device ring
+
+int current_bus_id(int* dev, char* bus) {
+  PACE_KV_TRY(hip_status(hipGetDevice(dev), "hipGetDevice"));
+  return hip_status(hipDeviceGetPCIBusId(bus, kBusIdBytes, *dev), "hipDeviceGetPCIBusId");
+}
+
+// Whether the channel has a device ring on the current GPU.
+int device_ring_here(pace_kv_channel* ch, bool* here) {
+  *here = false;
+  if (ch->ctl->dev_slot_bytes <= 0) return PACE_KV_OK;
+  int dev = -1;
+  char bus[kBusIdBytes] = {0};
+  PACE_KV_TRY(current_bus_id(&dev, bus));
+  *here = strncmp(bus, ch->ctl->dev_bus_id, kBusIdBytes) == 0;
+  return PACE_KV_OK;
+}
+
+int make_slot_events(pace_kv_channel* ch) {
+  const size_t n = ch->ctl->num_slots;
+  for (std::vector<hipEvent_t>* v : {&ch->dev_packed, &ch->dev_unpacked}) {
+    while (v->size() < n) {
+      hipEvent_t e = nullptr;
+      PACE_KV_TRY(hip_status(hipEventCreateWithFlags(&e, hipEventDisableTiming), "channel slot event"));
+      v->push_back(e);
+    }
+  }
+  return PACE_KV_OK;
+}
+
+// Maps the device ring into this process on the current GPU (once).
+int ring_ready(pace_kv_channel* ch) {
+  ChannelCtl* c = ch->ctl;
+  if (c->dev_slot_bytes <= 0) return fail(PACE_KV_ESTATE, "channel %s has no device ring", ch->name.c_str());
+  int dev = -1;
+  char bus[kBusIdBytes] = {0};
+  PACE_KV_TRY(current_bus_id(&dev, bus));
+  if (strncmp(bus, c->dev_bus_id, kBusIdBytes) != 0)
+    return fail(PACE_KV_ESTATE, "channel %s: its device ring is on the GPU at %.64s, the current GPU is at %s",
+                ch->name.c_str(), c->dev_bus_id, bus);
+  if (ch->dev_ring != nullptr) {
+    if (dev != ch->dev_device)
+      return fail(PACE_KV_ESTATE, "channel %s: device ring mapped on device %d, device %d is current",
+                  ch->name.c_str(), ch->dev_device, dev);
+    return make_slot_events(ch);
+  }
+  void* p = nullptr;
+  if (c->dev_owner_pid == static_cast<int32_t>(getpid())) {
+    std::lock_guard<std::mutex> lock(g_rings_mu);
+    auto it = g_rings.find(shm_inode(ch->fd));
+    if (it == g_rings.end())
+      return fail(PACE_KV_ESTATE, "channel %s: its device ring was allocated by this process and is freed",
+                  ch->name.c_str());
+    p = it->second;
+  } else {
+    PACE_KV_TRY(hip_status(hipIpcOpenMemHandle(&p, c->dev_handle, hipIpcMemLazyEnablePeerAccess),
+                           "hipIpcOpenMemHandle (channel device ring)"));
+    ch->dev_imported = true;
+  }
+  ch->dev_ring = static_cast<char*>(p);
+  ch->dev_device = dev;
+  return make_slot_events(ch);
+}
+
+char* dev_slot(pace_kv_channel* ch, uint32_t idx) {
+  return ch->dev_ring + static_cast<int64_t>(idx) * ch->ctl->dev_slot_bytes;
+}
+
+// Sender: waits until the record at position `pos` (head plus the records
+// reserved but not yet published) has a free slot.
+int acquire_slot_at(pace_kv_channel* ch, uint32_t pos, int timeout_ms, uint32_t* idx) {
+  ChannelCtl* c = ch->ctl;
+  PACE_KV_TRY(wait_for(ch, &c->tail, c->receiver,
+                       [&] { return pos - c->tail.load(std::memory_order_acquire) < c->num_slots; },
+                       timeout_ms, "a free slot"));
+  *idx = pos % c->num_slots;
+  return PACE_KV_OK;
+}
+
+// Sender: publishes device chunk `c` of message `id` once its pack into slot
+// idx has finished.
+int publish_dev_chunk(pace_kv_channel* ch, uint64_t id, int64_t c, const Chunking::Chunk& k, uint32_t idx) {
+  PACE_KV_TRY(hip_status(hipEventSynchronize(ch->dev_packed[idx]), "channel pack into the device ring"));
+  SlotRecord& r = ch->ctl->slots[idx];
+  r.kind = kDevData;
+  r.chunk = static_cast<uint32_t>(c);
+  r.msg_id = id;
+  r.offset = k.offset;
+  r.bytes = k.bytes;
+  publish(ch);
+  return PACE_KV_OK;
+}
+
+// Sender: packs every chunk straight into a device slot.  Chunk c is packed
+// before chunk c-1 is published, so the GPU has the next pack queued while
+// this thread waits for the previous one; at most one slot is reserved and
+// unpublished, so the receiver can always drain what precedes it.
+int send_device(pace_kv_channel* ch, const void* const* src_layers, int64_t pool_pages,
+                const int32_t* page_ids, const Chunking& k, uint64_t id, int timeout_ms, hipStream_t stream) {
+  const uint32_t first = ch->ctl->head.load(std::memory_order_relaxed);
+  uint32_t prev = 0;
+  for (int64_t c = 0; c < k.num_chunks; ++c) {
+    const Chunking::Chunk ck = k.at(c);
+    uint32_t idx = 0;
+    int rc = acquire_slot_at(ch, first + static_cast<uint32_t>(c), timeout_ms, &idx);
+    if (rc == PACE_KV_OK) {
+      const int64_t stride = k.layers_per_chunk > 0 ? k.layer_bytes : ck.bytes;
+      rc = pace_kv_pack(src_layers + ck.layer, ck.nl, pool_pages, page_ids + ck.j0, ck.nj, k.page_bytes,
+                        dev_slot(ch, idx), stride, nullptr, stream);
+    }
+    if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(ch->dev_packed[idx], stream), "channel send record");
+    if (rc == PACE_KV_OK && c > 0) rc = publish_dev_chunk(ch, id, c - 1, k.at(c - 1), prev);
+    if (rc) return abandon(ch, id, rc);
+    prev = idx;
+  }
+  if (k.num_chunks > 0) {
+    const int rc = publish_dev_chunk(ch, id, k.num_chunks - 1, k.at(k.num_chunks - 1), prev);
+    if (rc) return abandon(ch, id, rc);
+  }
+  return PACE_KV_OK;
+}
+
+// Receiver: a device chunk whose read failed still releases its slot, and
+// the rest of its message is dropped by the next header receive.
+int fail_rx(pace_kv_channel* ch, int rc) {
+  ch->rx_active = false;
+  release(ch);
+  return rc;
+}
+
+// Receiver: unpacks every chunk straight out of its device slot and releases
+// the slot once the unpack has finished, before waiting for the next chunk
+// (a receiver holding slots while it waits could stall a sender that has
+// reserved the next one).
+int recv_device(pace_kv_channel* ch, void* const* dst_layers, int64_t pool_pages, const int32_t* page_ids,
+                int32_t* err_count, int timeout_ms, hipStream_t stream) {
+  PACE_KV_TRY(ring_ready(ch));
+  const Chunking k = ch->rx_chunks;
+  while (ch->rx_active) {
+    uint32_t idx = 0;
+    Chunking::Chunk ck;
+    PACE_KV_TRY(next_chunk(ch, timeout_ms, &idx, &ck));
+    const int64_t stride = k.layers_per_chunk > 0 ? k.layer_bytes : ck.bytes;
+    int rc = pace_kv_unpack(dev_slot(ch, idx), stride, dst_layers + ck.layer, ck.nl, pool_pages,
+                            page_ids + ck.j0, ck.nj, k.page_bytes, err_count, stream);
+    if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(ch->dev_unpacked[idx], stream), "channel recv record");
+    if (rc == PACE_KV_OK)
+      rc = hip_status(hipEventSynchronize(ch->dev_unpacked[idx]), "channel unpack out of the device ring");
+    if (rc) return fail_rx(ch, rc);
+    finish_chunk(ch);
+  }
+  return PACE_KV_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int pace_kv_channel_create(const char* name, int64_t slot_bytes, int num_slots, int copy_threads,
-                           pace_kv_channel** out) {
+}  // extern "C"
+
+namespace {
+
+// Creates the ring (and, with dev_slot_bytes > 0, the device ring on the
+// current GPU); the magic goes in last.
+int create_channel(const char* name, int64_t slot_bytes, int num_slots, int copy_threads, int64_t dev_slot_bytes,
+                   pace_kv_channel** out) {
   PACE_KV_TRY(new_endpoint(name, copy_threads, out));
   pace_kv_channel* ch = *out;
   *out = nullptr;
@@ -644,6 +873,15 @@ int pace_kv_channel_create(const char* name, int64_t slot_bytes, int num_slots, 
   if (slot_bytes > (INT64_MAX / 2) / num_slots) {
     delete ch;
     return fail(PACE_KV_ERANGE, "channel: ring size overflows");
+  }
+  if (dev_slot_bytes < 0 || dev_slot_bytes % 4096 != 0) {
+    delete ch;
+    return fail(PACE_KV_EINVAL, "channel: dev_slot_bytes must be a non-negative multiple of 4096");
+  }
+  if (dev_slot_bytes > kMaxDeviceRing / num_slots) {
+    delete ch;
+    return fail(PACE_KV_ERANGE, "channel: a device ring of %d x %lld bytes exceeds %lld bytes", num_slots,
+                (long long)dev_slot_bytes, (long long)kMaxDeviceRing);
   }
   const int64_t data_offset = round_up(static_cast<int64_t>(sizeof(ChannelCtl)), 1 << 21);
   const int64_t total = data_offset + slot_bytes * num_slots;
@@ -683,10 +921,66 @@ int pace_kv_channel_create(const char* name, int64_t slot_bytes, int num_slots, 
     r->pidns.store(0);
     r->start.store(0);
   }
+  c->dev_slot_bytes = 0;
+  c->dev_owner_pid = 0;
+  if (dev_slot_bytes > 0) {
+    int dev = -1;
+    void* ring = nullptr;
+    rc = current_bus_id(&dev, c->dev_bus_id);
+    if (rc == PACE_KV_OK)
+      rc = hip_status(hipMalloc(&ring, static_cast<size_t>(dev_slot_bytes * num_slots)), "channel device ring");
+    if (rc == PACE_KV_OK) {
+      ch->dev_ring = static_cast<char*>(ring);
+      ch->dev_device = dev;
+      ch->dev_allocated = true;
+      std::lock_guard<std::mutex> lock(g_rings_mu);
+      g_rings[shm_inode(ch->fd)] = ch->dev_ring;
+    }
+    if (rc == PACE_KV_OK)
+      rc = hip_status(hipIpcGetMemHandle(&c->dev_handle, ring), "hipIpcGetMemHandle (channel device ring)");
+    if (rc == PACE_KV_OK) {
+      c->dev_slot_bytes = dev_slot_bytes;
+      c->dev_owner_pid = static_cast<int32_t>(getpid());
+      rc = make_slot_events(ch);
+    }
+    if (rc) {
+      destroy(ch);
+      return rc;
+    }
+  }
   std::atomic_thread_fence(std::memory_order_release);
   // The magic goes in last: an opener that sees it sees a complete block.
   __atomic_store_n(&c->magic, kMagic, __ATOMIC_RELEASE);
   *out = ch;
+  return PACE_KV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pace_kv_channel_create(const char* name, int64_t slot_bytes, int num_slots, int copy_threads,
+                           pace_kv_channel** out) {
+  return create_channel(name, slot_bytes, num_slots, copy_threads, 0, out);
+}
+
+int pace_kv_channel_create_device(const char* name, int64_t slot_bytes, int num_slots, int copy_threads,
+                                  int64_t dev_slot_bytes, pace_kv_channel** out) {
+  if (dev_slot_bytes <= 0) {
+    if (out) *out = nullptr;
+    return fail(PACE_KV_EINVAL, "channel: dev_slot_bytes must be a positive multiple of 4096");
+  }
+  return create_channel(name, slot_bytes, num_slots, copy_threads, dev_slot_bytes, out);
+}
+
+int pace_kv_channel_device_info(pace_kv_channel* ch, int64_t* dev_slot_bytes, int* on_current_gpu) {
+  if (ch == nullptr) return fail(PACE_KV_EINVAL, "channel is NULL");
+  if (dev_slot_bytes) *dev_slot_bytes = ch->ctl->dev_slot_bytes;
+  if (on_current_gpu) {
+    bool here = false;
+    PACE_KV_TRY(device_ring_here(ch, &here));
+    *on_current_gpu = here ? 1 : 0;
+  }
   return PACE_KV_OK;
 }
 
@@ -764,17 +1058,30 @@ int pace_kv_channel_send(pace_kv_channel* ch, const void* const* src_layers, int
                          void* stream_) {
   if (ch == nullptr) return fail(PACE_KV_EINVAL, "channel is NULL");
   std::lock_guard<std::mutex> lock(ch->send_mu);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  bool device = false;
+  if (num_layers > 0 && n_pages > 0) {
+    if (src_layers == nullptr || page_ids == nullptr) return fail(PACE_KV_EINVAL, "channel send: NULL argument");
+    PACE_KV_TRY(device_ring_here(ch, &device));
+  }
+  if (device) {
+    // Same GPU as the device ring: the payload never leaves HBM.
+    Chunking kd;
+    PACE_KV_TRY(make_chunking(num_layers, n_pages, page_bytes, ch->ctl->dev_slot_bytes, &kd));
+    PACE_KV_TRY(ring_ready(ch));
+    uint64_t id = 0;
+    PACE_KV_TRY(send_header(ch, num_layers, n_pages, page_bytes, meta, meta_bytes, timeout_ms, &id,
+                            kDevicePayload));
+    if (msg_id) *msg_id = id;
+    return send_device(ch, src_layers, pool_pages, page_ids, kd, id, timeout_ms, stream);
+  }
   Chunking k;
   PACE_KV_TRY(make_chunking(num_layers, n_pages, page_bytes, ch->ctl->slot_bytes, &k));
-  if (k.num_chunks > 0) {
-    if (src_layers == nullptr || page_ids == nullptr) return fail(PACE_KV_EINVAL, "channel send: NULL argument");
-    PACE_KV_TRY(staging_ready(ch, ch->tx));
-  }
+  if (k.num_chunks > 0) PACE_KV_TRY(staging_ready(ch, ch->tx));
   uint64_t id = 0;
   PACE_KV_TRY(send_header(ch, num_layers, n_pages, page_bytes, meta, meta_bytes, timeout_ms, &id));
   if (msg_id) *msg_id = id;
   Staging& s = ch->tx;
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
   // Chunk c: pack into device slot c%2 (caller stream), copy down to pinned
   // slot c%2 (copy stream); chunk c-1 is copied into the ring meanwhile.
   for (int64_t c = 0; c <= k.num_chunks; ++c) {
@@ -845,8 +1152,15 @@ int pace_kv_channel_recv_header(pace_kv_channel* ch, void* meta, int64_t meta_ca
   if (r.bytes > meta_cap || (r.bytes > 0 && meta == nullptr))
     return fail(PACE_KV_ERANGE, "channel %s: metadata needs %lld bytes, the buffer holds %lld (message kept)",
                 ch->name.c_str(), (long long)r.bytes, (long long)meta_cap);
+  const bool device = (r.flags & kDevicePayload) != 0;
+  if (device && ch->ctl->dev_slot_bytes <= 0) {
+    release(ch);
+    return fail(PACE_KV_ESTATE, "channel %s: message %llu is in device slots but the channel has none",
+                ch->name.c_str(), (unsigned long long)r.msg_id);
+  }
   Chunking k;
-  int rc = make_chunking(r.num_layers, r.n_pages, r.page_bytes, ch->ctl->slot_bytes, &k);
+  int rc = make_chunking(r.num_layers, r.n_pages, r.page_bytes,
+                         device ? ch->ctl->dev_slot_bytes : ch->ctl->slot_bytes, &k);
   if (rc) {
     release(ch);
     return rc;
@@ -859,6 +1173,7 @@ int pace_kv_channel_recv_header(pace_kv_channel* ch, void* meta, int64_t meta_ca
   ch->rx_msg = r.msg_id;
   ch->rx_chunks = k;
   ch->rx_next = 0;
+  ch->rx_device = device;
   ch->rx_active = k.num_chunks > 0;
   release(ch);
   return PACE_KV_OK;
@@ -871,6 +1186,9 @@ int pace_kv_channel_recv(pace_kv_channel* ch, void* const* dst_layers, int num_l
   std::lock_guard<std::mutex> lock(ch->recv_mu);
   PACE_KV_TRY(check_rx_shape(ch, num_layers, n_pages, page_bytes));
   if (dst_layers == nullptr || page_ids == nullptr) return fail(PACE_KV_EINVAL, "channel recv: NULL argument");
+  if (ch->rx_device)
+    return recv_device(ch, dst_layers, pool_pages, page_ids, err_count, timeout_ms,
+                       static_cast<hipStream_t>(stream_));
   PACE_KV_TRY(staging_ready(ch, ch->rx));
   const Chunking k = ch->rx_chunks;
   Staging& s = ch->rx;
@@ -922,11 +1240,21 @@ int pace_kv_channel_recv_host(pace_kv_channel* ch, void* payload, int64_t payloa
   if (payload != nullptr && payload_bytes != total)
     return fail(PACE_KV_EINVAL, "channel %s: message %llu holds %lld payload bytes, the buffer %lld",
                 ch->name.c_str(), (unsigned long long)ch->rx_msg, (long long)total, (long long)payload_bytes);
+  if (ch->rx_device && payload != nullptr) PACE_KV_TRY(ring_ready(ch));
   while (ch->rx_active) {
     uint32_t idx = 0;
     Chunking::Chunk ck;
     PACE_KV_TRY(next_chunk(ch, timeout_ms, &idx, &ck));
-    if (payload != nullptr) ch->pool->copy(static_cast<char*>(payload) + ck.offset, slot_data(ch, idx), ck.bytes);
+    if (payload != nullptr) {
+      char* to = static_cast<char*>(payload) + ck.offset;
+      if (ch->rx_device) {
+        const int rc = hip_status(hipMemcpy(to, dev_slot(ch, idx), static_cast<size_t>(ck.bytes),
+                                            hipMemcpyDeviceToHost), "channel copy out of the device ring");
+        if (rc) return fail_rx(ch, rc);
+      } else {
+        ch->pool->copy(to, slot_data(ch, idx), ck.bytes);
+      }
+    }
     finish_chunk(ch);
   }
   return PACE_KV_OK;

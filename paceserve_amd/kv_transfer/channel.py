@@ -73,13 +73,31 @@ class KVChannel:
 
     @classmethod
     def create(cls, name: str, slot_bytes: int = 32 * MiB, num_slots: int = 4,
-               copy_threads: int = 4) -> "KVChannel":
+               copy_threads: int = 4, device_slot_bytes: int = 0) -> "KVChannel":
         """Creates the ring (num_slots: a power of two in [2, 64]; slot_bytes:
-        a multiple of 4096) and returns the creating endpoint."""
+        a multiple of 4096) and returns the creating endpoint.  With
+        device_slot_bytes > 0 (a multiple of 4096, at most 1 GiB over all
+        slots) it also allocates a ring of device slots on the current GPU,
+        through which sends made on that GPU pass without leaving HBM."""
         handle = ctypes.c_void_p()
-        _native.check(_native.load().pace_kv_channel_create(name.encode(), int(slot_bytes), int(num_slots),
-                                                            int(copy_threads), ctypes.byref(handle)))
+        lib = _native.load()
+        if device_slot_bytes:
+            _native.check(lib.pace_kv_channel_create_device(name.encode(), int(slot_bytes), int(num_slots),
+                                                            int(copy_threads), int(device_slot_bytes),
+                                                            ctypes.byref(handle)))
+        else:
+            _native.check(lib.pace_kv_channel_create(name.encode(), int(slot_bytes), int(num_slots),
+                                                     int(copy_threads), ctypes.byref(handle)))
         return cls(handle.value, name)
+
+    def device_ring(self):
+        """(device slot bytes, 0 when the channel has no device ring; whether
+        the ring is on the current GPU, so that sends from here use it)."""
+        dsb = ctypes.c_int64()
+        here = ctypes.c_int()
+        _native.check(_native.load().pace_kv_channel_device_info(self._require(), ctypes.byref(dsb),
+                                                                 ctypes.byref(here)))
+        return dsb.value, bool(here.value)
 
     @classmethod
     def open(cls, name: str, copy_threads: int = 4, timeout: float = 30.0) -> "KVChannel":

@@ -3,6 +3,7 @@ order with their metadata, payloads larger than the ring streaming through
 it, layer- and page-sized chunks, another process as the sender, deadlines,
 closing, abandoned messages, draining, threads sharing an endpoint message by
 message, a peer process that dies mid-message, and argument errors."""
+import ctypes
 import os
 import subprocess
 import sys
@@ -494,3 +495,24 @@ def test_a_dead_receiver_ends_the_senders_wait():
         child.wait()
         t.join(timeout=30)
         tx.close()
+
+
+def test_device_ring_arguments_are_checked_before_any_device_call():
+    """Bad device-ring sizes are refused before the shared object or any HIP
+    call (this runs without a GPU)."""
+    lib = _native.load()
+    h = ctypes.c_void_p()
+    nm = f"pace_dev_args_{os.getpid()}".encode()
+    assert lib.pace_kv_channel_create_device(nm, 4096, 4, 1, 0, ctypes.byref(h)) == _native.PACE_KV_EINVAL
+    assert lib.pace_kv_channel_create_device(nm, 4096, 4, 1, 1000, ctypes.byref(h)) == _native.PACE_KV_EINVAL
+    assert lib.pace_kv_channel_create_device(nm, 4096, 4, 1, 512 << 20, ctypes.byref(h)) == _native.PACE_KV_ERANGE
+    assert b"exceeds 1073741824 bytes" in lib.pace_kv_last_error()
+    assert not os.path.exists(f"/dev/shm/{nm.decode()}")
+
+
+def test_host_channel_reports_no_device_ring():
+    ch = KVChannel.create(f"pace_nodev_{os.getpid()}", 4096, 2, 1)
+    try:
+        assert ch.device_ring() == (0, False)
+    finally:
+        ch.close()

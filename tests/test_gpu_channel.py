@@ -369,3 +369,167 @@ def test_helper_zero_fallback_and_repeated_ids(gpu):
         assert not dst_cache[l][10].any()
         assert torch.equal(words(dst_cache[l][20]), words(src_cache[l][5]))
         assert torch.equal(words(dst_cache[l][21]), words(src_cache[l][4]))
+
+
+# ------------------------------------------------------- same-GPU device ring
+
+def run_pair_device(dev_slot, send, recv, host_slot=4096, num_slots=4):
+    """run_pair over a channel with a device ring; the shared-memory slots are
+    4 KiB, so a payload of larger pages can only have taken the device ring."""
+    nm = name()
+    rx = KVChannel.create(nm, host_slot, num_slots, 2, device_slot_bytes=dev_slot)
+    tx = KVChannel.open(nm, 2, timeout=10)
+    assert rx.device_ring() == (dev_slot, True) and tx.device_ring() == (dev_slot, True)
+    out, errs = [], []
+
+    def sender():
+        try:
+            out.append(send(tx))
+        except Exception as e:                     # reported below
+            errs.append(repr(e))
+
+    t = threading.Thread(target=sender)
+    t.start()
+    recv_err = None
+    try:
+        recv(rx)
+    except Exception as e:                         # reported with the sender's
+        recv_err = repr(e)
+    finally:
+        t.join(timeout=60)
+        tx.close()
+        rx.close()
+    assert not errs and recv_err is None, f"sender: {errs}; receiver: {recv_err}"
+    return out[0] if out else None
+
+
+# (layers, pool pages, page shape, pages sent, device slot bytes): layer chunks,
+# page chunks (a layer larger than a slot), more layers than one launch
+# takes, one page, a two-slot ring
+DEVICE_CASES = [(32, 64, (2, 16, 8, 128), 20, 4 << 20, 4), (4, 300, (2, 16, 8, 128), 200, 1 << 20, 4),
+                (70, 16, (2, 16, 1, 64), 9, 1 << 20, 4), (2, 8, (2, 16, 8, 128), 1, 1 << 20, 4),
+                (8, 128, (2, 16, 8, 128), 100, 1 << 20, 2)]
+
+
+@pytest.mark.parametrize("L,pages,shape,n,slot,slots", DEVICE_CASES)
+def test_device_ring_in_one_process(gpu, L, pages, shape, n, slot, slots):
+    print(f"device ring case L={L} pages={pages} shape={shape} n={n} slot={slot} slots={slots}", flush=True)
+    src = rand_pool(L, pages, shape, torch.float16, gpu, 11)
+    dst = rand_pool(L, pages, shape, torch.float16, gpu, 12)
+    rng = np.random.default_rng(L + n + 1)
+    s_ids = rng.permutation(pages)[:n].tolist()
+    d_ids = rng.permutation(pages)[:n].tolist()
+    before = [words(d).clone() for d in dst]
+
+    def recv(rx):
+        for r in range(2):                          # two messages: the ring's slots are reused
+            h = rx.recv_header(timeout=30)
+            assert (h.meta, h.num_layers, h.n_pages) == (f"m{r}".encode(), L, n)
+            rx.recv(dst, d_ids, timeout=30)
+
+    def send(tx):
+        for r in range(2):
+            tx.send(src, s_ids, f"m{r}".encode(), timeout=30)
+
+    run_pair_device(slot, send, recv, num_slots=slots)
+    torch.cuda.synchronize()
+    si, di = torch.tensor(s_ids, device=gpu), torch.tensor(d_ids, device=gpu)
+    keep = torch.tensor(sorted(set(range(pages)) - set(d_ids)), device=gpu, dtype=torch.long)
+    for l in range(L):
+        assert torch.equal(words(dst[l])[di], words(src[l])[si]), f"layer {l}"
+        assert torch.equal(words(dst[l])[keep], before[l][keep]), f"layer {l} untouched pages"
+
+
+def test_device_ring_to_host_discard_and_host_messages(gpu):
+    """A device-slot message received into host memory, one discarded, and a
+    host payload (shared-memory slots) between them, on one channel."""
+    L, pages, shape, n = 5, 40, (2, 16, 8, 128), 17
+    src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 13)
+    ids = np.random.default_rng(7).permutation(pages)[:n].tolist()
+    want = torch.stack([s[torch.tensor(ids, device=gpu)] for s in src]).cpu()
+    got = torch.empty((L, n) + shape, dtype=torch.bfloat16)
+    back = torch.empty_like(got)
+
+    def send(tx):
+        tx.send(src, ids, b"a", timeout=30)        # device slots
+        tx.send(src, ids, b"b", timeout=30)        # device slots, discarded
+        tx.send_host(want, b"c", timeout=30)       # shared-memory slots
+
+    def recv(rx):
+        assert rx.recv_header(timeout=30).meta == b"a"
+        rx.recv_host(got, timeout=30)
+        assert rx.recv_header(timeout=30).meta == b"b"
+        rx.discard(timeout=30)
+        assert rx.recv_header(timeout=30).meta == b"c"
+        rx.recv_host(back, timeout=30)
+
+    run_pair_device(1 << 20, send, recv, host_slot=1 << 20)
+    assert torch.equal(words(got), words(want))
+    assert torch.equal(words(back), words(want))
+
+
+DEVICE_PEER = r"""
+import sys, torch
+sys.path.insert(0, {root!r})
+from paceserve_amd.kv_transfer.channel import KVChannel
+dev = torch.device("cuda", 0)
+g = torch.Generator(device=dev).manual_seed(78)
+src = [torch.randn((128, 2, 16, 8, 128), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+       for _ in range(32)]
+ch = KVChannel.open({name!r}, 2, timeout=60)
+assert ch.device_ring() == ({dev_slot}, True), ch.device_ring()
+if {role!r} == "send":
+    for r in range(3):
+        ids = list(range(r, 128, 3))[:40]
+        ch.send(src, ids, ("request %d" % r).encode(), timeout=60)
+else:
+    dst = [torch.zeros_like(s) for s in src]
+    for r in range(3):
+        h = ch.recv_header(timeout=60)
+        assert h.meta == ("request %d" % r).encode() and h.n_pages == 40, h
+        ch.recv(dst, list(range(40 * r, 40 * r + 40)), timeout=60)
+    torch.cuda.synchronize()
+    for r in range(3):
+        s_ids = torch.tensor(list(range(r, 128, 3))[:40], device=dev)
+        d_ids = torch.arange(40 * r, 40 * r + 40, device=dev)
+        for l in range(32):
+            assert torch.equal(dst[l][d_ids].view(torch.int16), src[l][s_ids].view(torch.int16)), (r, l)
+print("peer done", flush=True)
+ch.close()
+"""
+
+
+@pytest.mark.parametrize("peer", ["send", "recv"])
+def test_device_ring_with_a_peer_process(gpu, peer):
+    """The ring's creator on one side, a process that opens the exported
+    ring on the other: the opener sends (its packs write the creator's
+    allocation) or receives (its unpacks read it)."""
+    nm = name()
+    dev_slot = 4 << 20                                  # 40 pages x 64 KiB: whole layers, 4 MiB slots
+    ch = KVChannel.create(nm, 4096, 4, 2, device_slot_bytes=dev_slot)
+    child = subprocess.Popen([sys.executable, "-c",
+                              DEVICE_PEER.format(root=str(ROOT), name=nm, dev_slot=dev_slot, role=peer)])
+    try:
+        g = torch.Generator(device=gpu).manual_seed(78)
+        src = [torch.randn((128, 2, 16, 8, 128), generator=g, device=gpu, dtype=torch.float32).to(torch.bfloat16)
+               for _ in range(32)]
+        dst = [torch.zeros_like(s) for s in src]
+        for r in range(3):
+            if peer == "send":
+                h = ch.recv_header(timeout=120)
+                assert h.meta == f"request {r}".encode() and h.n_pages == 40
+                ch.recv(dst, list(range(40 * r, 40 * r + 40)), timeout=60)
+            else:
+                ch.send(src, list(range(r, 128, 3))[:40], f"request {r}".encode(), timeout=120)
+        torch.cuda.synchronize()
+        assert child.wait(timeout=60) == 0
+    finally:
+        if child.poll() is None:
+            child.kill()
+        ch.close()
+    if peer == "send":
+        for r in range(3):
+            s_ids = torch.tensor(list(range(r, 128, 3))[:40], device=gpu)
+            d_ids = torch.arange(40 * r, 40 * r + 40, device=gpu)
+            for l in range(32):
+                assert torch.equal(words(dst[l][d_ids]), words(src[l][s_ids])), f"request {r} layer {l}"
