@@ -34,6 +34,7 @@ import os
 import statistics
 import sys
 import time
+from array import array
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -820,23 +821,33 @@ def run_promote(dev, steps=100, warmup=10):
     dst = w.dst_pool(dev)
     host = torch.empty(w.payload_bytes, dtype=torch.uint8, pin_memory=True)
     out = {}
-    # "buffer"/"fused": Python planner + ops; "*_native": one pace_kv_promote call
-    for mode in ("buffer", "fused", "pinned", "buffer_native", "fused_native"):
-        native = mode.endswith("_native")
+    # The request's block table as a scheduler built on the native allocator
+    # holds it: int32 ids and int64 offsets (CSR), no Python lists.
+    csr_ids = array("i", w.src_tables[0])
+    csr_indptr = array("q", (0, len(csr_ids)))
+    # "buffer"/"fused": Python planner + ops; "*_native": one pace_kv_promote
+    # call from KVMigrator.promote (list-of-lists block tables);
+    # "buffer_native_csr": the same call from KVMigrator.promote_native (CSR)
+    for mode in ("buffer", "fused", "pinned", "buffer_native", "fused_native", "buffer_native_csr"):
+        native = "_native" in mode
         alloc = (NativeBlockAllocator if native else BlockAllocator)(w.shape.page_size, w.dst_pool_pages)
         mig = migrate.KVMigrator(src, dst, alloc)
-        kind = mode.replace("_native", "")
+        kind = mode.split("_")[0]
         lat = []
         n_iter = warmup + steps
         for i in range(n_iter):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            plan = mig.promote(w.src_tables, mode=kind, host_buf=host if kind == "pinned" else None)
+            if mode == "buffer_native_csr":
+                got = mig.promote_native(csr_ids, csr_indptr, mode=kind)
+            else:
+                got = mig.promote(w.src_tables, mode=kind, host_buf=host if kind == "pinned" else None)
             ev = torch.cuda.Event()
             ev.record()
             ev.synchronize()
             t1 = time.perf_counter()
-            for t in plan.dst_tables:             # return the pages (outside the timing)
+            # return the pages (outside the timing)
+            for t in (got.dst_tables if mode != "buffer_native_csr" else [got.tolist()]):
                 alloc.free_many(reversed(t))
             if i >= warmup:
                 lat.append((t1 - t0) * 1e6)
@@ -867,7 +878,8 @@ def run_promote(dev, steps=100, warmup=10):
     # the metric's promote latency: allocation + remap + id upload + pack +
     # unpack, through the single library call
     out["p50_us"] = out["buffer_native"]["p50_us"]
-    out["p50_mode"] = "buffer_native (pace_kv_promote: plan, id upload, pack, unpack)"
+    out["p50_mode"] = ("buffer_native (KVMigrator.promote of list block tables -> pace_kv_promote: plan, ids, "
+                       "pack, unpack)")
     return out
 
 

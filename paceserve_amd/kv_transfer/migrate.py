@@ -25,6 +25,7 @@ from __future__ import annotations
 
 import itertools
 import threading
+from array import array
 from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
@@ -82,6 +83,22 @@ def plan_batch(src_tables: Sequence[Sequence[int]], src_num_pages: int, dst_allo
     return MigrationPlan(src_ids, dst_ids, dst_tables, indptr)
 
 
+def _csr_of_int32_tables(src_tables: Sequence[Sequence[int]]):
+    """(ids array('i'), indptr array('q'), counts) of a batch whose ids all
+    fit int32, or None (an id that does not, or is not an int).  The ids are
+    not range-checked here: the library checks them before it allocates."""
+    try:
+        if len(src_tables) == 1:
+            ids = array("i", src_tables[0])
+            counts = [len(ids)]
+        else:
+            counts = [len(t) for t in src_tables]
+            ids = array("i", itertools.chain.from_iterable(src_tables))
+    except (OverflowError, TypeError):
+        return None
+    return ids, array("q", (0, *itertools.accumulate(counts))), counts
+
+
 def flatten_tables(src_tables: Sequence[Sequence[int]], num_pages: int):
     """CSR form of a batch of source block tables: (ids int32, indptr int64,
     counts).  Ids follow torch advanced-indexing rules, as normalize_page_ids
@@ -122,6 +139,7 @@ class KVMigrator:
         # stream's work, since the transfer buffer is shared.
         self._lock = threading.RLock()
         self._buf_stream: Optional[torch.cuda.Stream] = None
+        self._buf_handle: Optional[int] = None
 
     # ------------------------------------------------------------ planning
 
@@ -141,16 +159,20 @@ class KVMigrator:
 
     # ------------------------------------------------------------ movement
 
-    def _order_after_last_user(self) -> None:
+    def _order_after_last_user(self) -> int:
         """Orders the current stream after the stream that last used the
         transfer buffer (and lets torch's allocator know the buffer is used
-        here), when the two differ.  Caller holds the lock."""
-        stream = torch.cuda.current_stream(self.src.device)
-        if self._buf_stream is not None and self._buf_stream != stream:
-            stream.wait_stream(self._buf_stream)
-            if self._buf is not None:
-                self._buf.record_stream(stream)
-        self._buf_stream = stream
+        here), when the two differ; returns the current stream's handle.
+        Caller holds the lock."""
+        handle = ops._stream_handle(self.src.device)
+        if handle != self._buf_handle:
+            stream = torch.cuda.current_stream(self.src.device)
+            if self._buf_stream is not None:
+                stream.wait_stream(self._buf_stream)
+                if self._buf is not None:
+                    self._buf.record_stream(stream)
+            self._buf_stream, self._buf_handle = stream, handle
+        return handle
 
     def _buffer(self, layers: int, n: int) -> torch.Tensor:
         """A [layers, n, *page_shape] view of the migrator's transfer buffer
@@ -210,36 +232,36 @@ class KVMigrator:
     def promote_native(self, src_ids, indptr, dst_pages=None, mode: str = "fused",
                        layers_per_chunk: Optional[int] = None):
         """One library call (pace_kv_promote) for a CSR batch: src_ids int32
-        (ids in [0, num_pages)), indptr int64.  Needs a NativeBlockAllocator.
+        (ids in [0, num_pages)), indptr int64, as numpy arrays or
+        array.array('i') / array.array('q').  Needs a NativeBlockAllocator.
         Returns the destination tables concatenated (int32 array)."""
+        tables, total = self._promote_native(src_ids, indptr, dst_pages, mode, layers_per_chunk, False)
+        return np.frombuffer(tables, dtype=np.int32, count=total).copy()
+
+    def _promote_native(self, src_ids, indptr, dst_pages, mode, layers_per_chunk, source_range_ok: bool):
         if not isinstance(self.dst_allocator, NativeBlockAllocator):
             raise TypeError("promote_native needs a NativeBlockAllocator")
-        with self._lock:
-            return self._promote_native(src_ids, indptr, dst_pages, mode, layers_per_chunk)
-
-    def _promote_native(self, src_ids, indptr, dst_pages, mode, layers_per_chunk):
-        if self._promoter is None:
-            self._promoter = ops.Promoter(self.src.device)
         if mode not in ("buffer", "fused"):
             raise ValueError(f"promote_native supports modes 'buffer' and 'fused', not {mode!r}")
-        self._order_after_last_user()
-        src_ids = np.ascontiguousarray(src_ids, dtype=np.int32)
-        indptr = np.ascontiguousarray(indptr, dtype=np.int64)
+        if not isinstance(src_ids, array):
+            src_ids = np.ascontiguousarray(src_ids, dtype=np.int32)
+        if not isinstance(indptr, array):
+            indptr = np.ascontiguousarray(indptr, dtype=np.int64)
+        counts = None if dst_pages is None else np.ascontiguousarray(dst_pages, dtype=np.int32)
         n = int(indptr[-1])
-        if dst_pages is None:
-            counts, total = None, n
-        else:
-            counts = np.ascontiguousarray(dst_pages, dtype=np.int32)
-            total = int(counts.sum())
-        buf_ptr, stride, blayers = None, 0, 0
-        if mode == "buffer":
-            # The migrator's own view: contiguous [k, n, *page_shape] of the
-            # pools' dtype on their device, so it needs no further checks.
-            k = layers_per_chunk or self.chunk_layers(n)
-            buf = self._buffer(min(k, self.src.num_layers), n)
-            buf_ptr, stride, blayers = buf.data_ptr(), n * self.src.page_bytes, int(buf.shape[0])
-        return self._promoter._launch(self.src, self.dst, self.dst_allocator, src_ids, indptr, counts, total,
-                                      buf_ptr, stride, blayers)
+        with self._lock:
+            if self._promoter is None:
+                self._promoter = ops.Promoter(self.src.device)
+            stream = self._order_after_last_user()
+            buf_ptr, stride, blayers = None, 0, 0
+            if mode == "buffer":
+                # The migrator's own view: contiguous [k, n, *page_shape] of the
+                # pools' dtype on their device, so it needs no further checks.
+                k = layers_per_chunk or self.chunk_layers(n)
+                buf = self._buffer(min(k, self.src.num_layers), n)
+                buf_ptr, stride, blayers = buf.data_ptr(), n * self.src.page_bytes, int(buf.shape[0])
+            return self._promoter._launch(self.src, self.dst, self.dst_allocator, src_ids, indptr, counts,
+                                          buf_ptr, stride, blayers, None, stream, source_range_ok)
 
     def promote(self, src_tables: Sequence[Sequence[int]], dst_pages: Optional[Sequence[int]] = None,
                 mode: str = "buffer", layers_per_chunk: Optional[int] = None,
@@ -249,9 +271,20 @@ class KVMigrator:
         NativeBlockAllocator, the device modes run as one library call."""
         if isinstance(self.dst_allocator, NativeBlockAllocator) and mode in ("buffer", "fused"):
             # Only the work before the library call adds latency: the plan
-            # below is built while the GPU copies.
-            src_ids, indptr, counts = flatten_tables(src_tables, self.src.num_pages)
-            tables = self.promote_native(src_ids, indptr, dst_pages, mode, layers_per_chunk).tolist()
+            # below is built while the GPU copies.  Tables of int32 ids in
+            # range go to the library as they are; the library refuses any
+            # other id before allocating, and the ids are then normalised
+            # with torch's indexing rules (negative ids count from the end)
+            # or rejected with its IndexError.
+            tables = None
+            fast = _csr_of_int32_tables(src_tables)
+            if fast is not None:
+                src_ids, indptr, counts = fast
+                tables, total = self._promote_native(src_ids, indptr, dst_pages, mode, layers_per_chunk, True)
+            if tables is None:
+                src_ids, indptr, counts = flatten_tables(src_tables, self.src.num_pages)
+                tables, total = self._promote_native(src_ids, indptr, dst_pages, mode, layers_per_chunk, False)
+            tables = tables[:total].tolist()
             sizes = counts if dst_pages is None else list(dst_pages)
             dst_tables, dst_ids, pos = [], [], 0
             for n, m in zip(counts, sizes):

@@ -153,3 +153,26 @@ def test_one_migrator_from_threads_on_their_own_streams(gpu):
         for plan in plans.values():
             for t in plan.dst_tables:
                 alloc.free_many(reversed(t))
+
+
+def test_native_promote_normalises_negative_ids_and_rejects_out_of_range(gpu):
+    """Tables go to the library as they are; an id the library refuses
+    (negative, or past the pool) sends the call through torch's indexing
+    rules: a negative id counts from the end, an id outside [-N, N) raises
+    IndexError with no page allocated."""
+    src, dst_a = pools(gpu, 21)
+    _, dst_b = pools(gpu, 21)
+    table = [5, -1, 700, -2048, 3]
+    a = migrate.KVMigrator(src, dst_a, NativeBlockAllocator(16, POOL))
+    b = migrate.KVMigrator(src, dst_b, NativeBlockAllocator(16, POOL))
+    pa = a.promote([table], mode="buffer")
+    pb = b.promote([[t % POOL for t in table]], mode="buffer")
+    torch.cuda.synchronize()
+    assert pa.src_ids == [5, POOL - 1, 700, 0, 3] and pa.dst_tables == pb.dst_tables
+    for l in range(SHAPE.num_layers):
+        assert torch.equal(words(dst_a.layers[l]), words(dst_b.layers[l])), f"layer {l}"
+    free_before = a.dst_allocator.free_blocks
+    for bad in ([1, POOL], [-POOL - 1], [2**40]):
+        with pytest.raises(IndexError, match="out of bounds for dimension 0 with size 2048"):
+            a.promote([bad], mode="buffer")
+        assert a.dst_allocator.free_blocks == free_before
