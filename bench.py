@@ -339,11 +339,14 @@ def run_append(dev, steps: int = 50, warmup: int = 5) -> dict:
     Llama-3-8B layer cache [2048 pages, 2, 16, 8, 128] bf16:
       prefill: 16 requests x 1024 new tokens (16384 K and V rows);
       decode:  256 requests x 1 new token, sequences of 1..64 tokens.
-    Algorithmic bytes per launch: each appended K and V row (8 * 128 * 2 B)
-    read once and written once.  Kernel time comes from replays of a HIP
-    graph of launches; the eager time per Python call is reported beside it.
-    Every appended row is checked against torch's own indexing of the cache
-    after the replays."""
+    Two forms: the reference's (positions precomputed by
+    get_batch_indices_positions, then the append) and the fused one
+    (append_paged_kv_cache_indptr: positions derived in the same launch, the
+    whole per-layer step in one call).  Algorithmic bytes per launch: each
+    appended K and V row (8 * 128 * 2 B) read once and written once.  Kernel
+    time comes from replays of a HIP graph of launches; the eager time per
+    Python call is reported beside it.  Every appended row is checked
+    against torch's own indexing of the cache after the replays."""
     import torch
 
     from paceserve_amd.kv_transfer import append as ap
@@ -360,6 +363,35 @@ def run_append(dev, steps: int = 50, warmup: int = 5) -> dict:
         "prefill": ([1024] * 16, [1024] * 16),
         "decode": (torch.randint(1, 65, (256,), generator=lens_rng).tolist(), [1] * 256),
     }
+
+    def timed(fn, reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps * 1e3
+
+    def graph_us(fn):
+        # The Python wrapper costs more host time per call than a decode
+        # launch takes on the GPU, so the kernel is timed from a HIP graph of
+        # `steps` launches, replayed; it allocates nothing and records no
+        # memset, and every replay rewrites the same rows.
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            fn()
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            for _ in range(steps):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        return timed(graph.replay, 5) / steps
+
     for name, (seq_lens, new) in cases.items():
         npages = [-(-n // P) for n in seq_lens]
         kv_indptr = torch.tensor([0] + list(torch.tensor(npages).cumsum(0).tolist()), dtype=torch.int32, device=dev)
@@ -375,48 +407,46 @@ def run_append(dev, steps: int = 50, warmup: int = 5) -> dict:
         def launch():
             ap.append_paged_kv_cache(key, value, bi, pos, cache, kv_indices, kv_indptr, last)
 
-        for _ in range(warmup):
-            launch()
-        torch.cuda.synchronize()
+        def fused():
+            ap.append_paged_kv_cache_indptr(key, value, append_indptr, cache, kv_indices, kv_indptr, last)
 
-        def timed(fn, reps):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for _ in range(reps):
-                fn()
-            b.record(stream)
-            torch.cuda.synchronize()
-            return a.elapsed_time(b) / reps * 1e3
-
-        eager_us = timed(launch, steps)
-        # The Python wrapper costs more host time per call than a decode
-        # launch takes on the GPU, so the kernel is timed from a HIP graph of
-        # `steps` launches, replayed; it allocates nothing and records no
-        # memset, and every replay rewrites the same rows.
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream(dev)
-        side.wait_stream(stream)
-        with torch.cuda.stream(side):
-            launch()
-        stream.wait_stream(side)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph):
-            for _ in range(steps):
-                launch()
-        graph.replay()
-        torch.cuda.synchronize()
-        us = timed(graph.replay, 5) / steps
-        alg = 4 * nnz * row
-        # every appended row sits where the cache's page table puts it
         b_l, p_l = bi.long(), pos.long()
         page_t = kv_indices.long()[kv_indptr.long()[b_l] + p_l // P]
-        ok = torch.equal(cache[page_t, 0, p_l % P].view(torch.int16), key.view(torch.int16)) and \
-            torch.equal(cache[page_t, 1, p_l % P].view(torch.int16), value.view(torch.int16))
-        out[name] = {"tokens": nnz, "requests": len(seq_lens), "us_per_launch": round(us, 2),
-                     "eager_us_per_call": round(eager_us, 2),
-                     "algorithmic_bytes_per_launch": alg, "gbs": round(alg / (us * 1e-6) / 1e9, 1),
-                     "frac_of_hbm_peak": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "verified": bool(ok)}
-        log(f"append {name}: {nnz} tokens, {us:.2f} us per launch, {out[name]['gbs']} GB/s, verified {ok}")
+
+        def landed():
+            return torch.equal(cache[page_t, 0, p_l % P].view(torch.int16), key.view(torch.int16)) and \
+                torch.equal(cache[page_t, 1, p_l % P].view(torch.int16), value.view(torch.int16))
+
+        alg = 4 * nnz * row
+        res = {"tokens": nnz, "requests": len(seq_lens), "algorithmic_bytes_per_launch": alg}
+        for form, fn in (("", launch), ("fused_", fused)):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            eager_us = timed(fn, steps)
+            cache.zero_()
+            us = graph_us(fn)
+            ok = landed()
+            res[f"{form}us_per_launch"] = round(us, 2)
+            res[f"{form}eager_us_per_call"] = round(eager_us, 2)
+            res[f"{form}gbs"] = round(alg / (us * 1e-6) / 1e9, 1)
+            res[f"{form}frac_of_hbm_peak"] = round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+            res[f"{form}verified"] = bool(ok)
+            log(f"append {name} {form or 'two-call '}: {nnz} tokens, {us:.2f} us per launch, "
+                f"{res[f'{form}gbs']} GB/s, eager {eager_us:.2f} us per call, verified {ok}")
+        # the reference's whole per-layer step, eager: get_seq_lens (torch),
+        # get_batch_indices_positions, append_paged_kv_cache
+        def step():
+            s_l = ap.get_seq_lens(kv_indptr, last, P)
+            b_i, p_s = ap.get_batch_indices_positions(append_indptr, s_l, nnz)
+            ap.append_paged_kv_cache(key, value, b_i, p_s, cache, kv_indices, kv_indptr, last)
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        res["three_call_step_eager_us"] = round(timed(step, steps), 2)
+        res["verified"] = res["verified"] and res["fused_verified"]
+        out[name] = res
     return out
 
 
@@ -1166,6 +1196,36 @@ def summarize_copies(copy_csv: str, kernel_csv: str, bench_json: str, command: s
     return "\n".join(out) + "\n"
 
 
+def summarize_kernel_pmc(kernel: str, command: str, csvs: list) -> str:
+    """Markdown table of rocprofv3 --pmc counter values per dispatch for the
+    kernels whose names contain `kernel` (alternatives separated by '|'),
+    grouped by kernel and grid size (each counter's mean over the dispatches
+    of a group), from one or more counter-collection CSVs (one pass each).
+    `command` may hold several commands, one per line."""
+    groups = {}
+    wanted = kernel.split("|")
+    for path in csvs:
+        for r in _rows(path):
+            name = r["Kernel_Name"]
+            if not any(k in name for k in wanted):
+                continue
+            short = name.split("(anonymous namespace)::", 1)[-1].split("(")[0]
+            if short.startswith("__amd_rocclr"):
+                short = short.split("<")[0]
+            key = (short, int(r.get("Grid_Size", 0) or 0))
+            groups.setdefault(key, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    counters = sorted({c for g in groups.values() for c in g})
+    out = [f"# rocprofv3 counters per dispatch: {kernel}", "", "Command (repo root, one MI355X; one pass per CSV):",
+           "", "```", "export TMPDIR=/tmp", command, "```", "",
+           "| kernel | grid size (threads) | dispatches | " + " | ".join(counters) + " |",
+           "|---|---|---|" + "---|" * len(counters)]
+    for (short, grid), vals in sorted(groups.items(), key=lambda kv: kv[0][1]):
+        n = max(len(v) for v in vals.values())
+        cells = [f"{statistics.mean(vals[c]):.4g}" if c in vals else "" for c in counters]
+        out.append(f"| {short} | {grid} | {n} | " + " | ".join(cells) + " |")
+    return "\n".join(out) + "\n"
+
+
 def pmc_markdown(traffic_json: str) -> str:
     """Markdown form of a --summarize-pmc result (the committed summary)."""
     t = _json(traffic_json)
@@ -1239,6 +1299,19 @@ def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-promote":
         # python bench.py --summarize-promote KERNEL_TRACE.csv BENCH_LINE.json "COMMAND"
         print(summarize_promote(sys.argv[2], sys.argv[3], sys.argv[4]), end="")
+        return
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-kernel-pmc":
+        # python bench.py --summarize-kernel-pmc KERNEL_SUBSTRING "COMMAND" COUNTERS.csv [COUNTERS.csv ...]
+        print(summarize_kernel_pmc(sys.argv[2], sys.argv[3], sys.argv[4:]), end="")
+        return
+    if len(sys.argv) > 1 and sys.argv[1] == "--only-append":
+        # python bench.py --only-append: the paged-append leg alone (for profiling)
+        import torch
+
+        from paceserve_amd import _native
+
+        _native.load()
+        print(json.dumps({"append": run_append(torch.device("cuda", 0))}), flush=True)
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-copies":
         # python bench.py --summarize-copies MEMORY_COPY_TRACE.csv KERNEL_TRACE.csv BENCH_LINE.json "COMMAND"

@@ -270,6 +270,31 @@ int pace_kv_append(const void* keys, const void* values, int64_t token_stride_by
                    int32_t* err_count, void* stream);
 
 /*
+ * The same append with each token's request and position derived in the
+ * launch itself from the request offsets, so one launch does what
+ * get_seq_lens, get_batch_indices_positions and append_paged_kv_cache do:
+ *   token i of request b (append_indptr[b] <= i < append_indptr[b+1]),
+ *   seq_len = max(kv_indptr[b+1] - kv_indptr[b] - 1, 0) * page_size + kv_last_page_len[b],
+ *   pos = seq_len - (append_indptr[b+1] - append_indptr[b]) + (i - append_indptr[b]).
+ * append_indptr, kv_indptr (batch_size + 1 entries), kv_last_page_len
+ * (batch_size) and kv_indices are device int32 arrays.  A token outside
+ * every request, or whose slot or page is out of range, is skipped and
+ * counted in err_count.
+ *
+ * Replaces the three calls the reference makes for each layer
+ * (paceserve/model_executor/attention/flashinfer_attention_wrapper.py:
+ * 241-255).
+ */
+int pace_kv_append_indptr(const void* keys, const void* values,
+                          int64_t token_stride_bytes, int64_t nnz,
+                          const int32_t* append_indptr, int batch_size,
+                          void* cache, int64_t num_pages,
+                          const int32_t* kv_indices, int64_t num_indices,
+                          const int32_t* kv_indptr,
+                          const int32_t* kv_last_page_len, int page_size,
+                          int64_t row_bytes, int32_t* err_count, void* stream);
+
+/*
  * Request index and sequence position of every appended token (device):
  *   for append_indptr[b] <= i < append_indptr[b+1]:
  *     batch_indices[i] = b,

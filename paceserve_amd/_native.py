@@ -48,6 +48,9 @@ SIGNATURES = {
     "pace_kv_append": (
         c_int, [_VP, _VP, c_int64, c_int64, _VP, _VP, c_int, _VP, c_int64, _VP, c_int64, _VP, c_int,
                 c_int64, _VP, _VP]),
+    "pace_kv_append_indptr": (
+        c_int, [_VP, _VP, c_int64, c_int64, _VP, c_int, _VP, c_int64, _VP, c_int64, _VP, _VP, c_int, c_int64,
+                _VP, _VP]),
     "pace_kv_batch_indices_positions": (c_int, [_VP, _VP, c_int, c_int64, _VP, _VP, _VP]),
     "pace_kv_allocator_create": (c_int, [c_int64, _VP, c_int64, POINTER(c_void_p)]),
     "pace_kv_allocator_destroy": (c_int, [_VP]),

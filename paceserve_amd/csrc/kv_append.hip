@@ -10,8 +10,17 @@
 //   pos = seq_len[b] - (append_indptr[b+1] - append_indptr[b]) + (i - append_indptr[b])
 //   cache[kv_indices[kv_indptr[b] + pos / P]][0 (K) | 1 (V)][pos % P] = key[i] | value[i]
 //
-// One wave64 workgroup copies one 1 KiB row of one token's K or V (lanes move
-// 16-byte vectors, as in the page copy).  Every index is checked: a token whose
+// pace_kv_append takes b and pos per token (get_batch_indices_positions);
+// pace_kv_append_indptr derives them in the same launch from append_indptr,
+// kv_indptr and kv_last_page_len, so a layer's append is one launch.
+//
+// One wave64 workgroup copies one token's K or V row (or a 16 KiB chunk of a
+// longer row): every lane loads its vectors of the row, then stores them,
+// with the page copy's device-scope write-through store.  Measured on MI355X
+// (Llama-3-8B rows of 2 KiB, 16 x 1024 tokens): 20.6 us per launch against
+// 23.3-24.5 us for a wave per 1 KiB half row with nontemporal stores, and
+// 22.3 us for the half-row waves with these stores; nontemporal
+// write-through stores ran at 23.9 us.  Every index is checked: a token whose
 // request, page slot or page id is out of range is skipped and counted.
 #include "internal.h"
 
@@ -20,7 +29,8 @@ namespace {
 
 constexpr int kThreads = 64;
 constexpr int kVecBytes = 16;
-constexpr int kRowBytes = kThreads * kVecBytes;
+// Longest row one wave carries: 16 vectors of 16 bytes per lane.
+constexpr int kMaxVecsPerLane = 16;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -28,8 +38,10 @@ struct AppendParams {
   const char* key;
   const char* value;
   int64_t token_stride;      // bytes between tokens in key / value
-  const int32_t* batch_indices;
+  const int32_t* batch_indices;  // precomputed token -> request (or nullptr: derive from append_indptr)
   const int32_t* positions;
+  const int32_t* append_indptr;  // batch_size + 1 entries (the fused form)
+  const int32_t* kv_last_page_len;  // batch_size entries (the fused form)
   const int32_t* kv_indices;
   const int32_t* kv_indptr;  // batch_size + 1 entries
   int64_t num_indices;       // entries of kv_indices
@@ -39,50 +51,106 @@ struct AppendParams {
   uint32_t batch_size;
   uint32_t num_pages;
   uint32_t page_size;
-  uint32_t chunks_per_row;   // ceil(row_bytes / kRowBytes)
+  uint32_t chunks_per_row;   // ceil(row_vecs / (V * 64))
   uint32_t total_items;      // nnz * 2 * chunks_per_row
   uint32_t row_vecs;         // row_bytes / 16
 };
 
-template <bool GUARD>
+// A store of more than 64 bits reads its data registers after it issues; the
+// asm carries the wait states the compiler cannot add for it (s_nop 1).
+__device__ __forceinline__ void store_row_vec(u32x4* d, const u32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" : : "v"(d), "v"(v) : "memory");
+}
+
+// Request of token i in the fused form: the largest b < batch_size with
+// append_indptr[b] <= i, found by the whole wave at once: each lane loads
+// one entry of each block of 64 (four blocks per round, loaded before any is
+// tested, so up to 256 requests cost one load latency), and the entries that
+// pass are counted; -1 if none.
+__device__ __forceinline__ int32_t request_of(const AppendParams& p, int32_t i) {
+  constexpr int kBlocks = 4;
+  uint32_t count = 0;
+  for (uint32_t base = 0; base < p.batch_size; base += kBlocks * kThreads) {
+    int32_t x[kBlocks];
+#pragma unroll
+    for (int k = 0; k < kBlocks; ++k) {
+      const uint32_t e = base + k * kThreads + threadIdx.x;
+      x[k] = e < p.batch_size ? p.append_indptr[e] : INT32_MAX;
+    }
+#pragma unroll
+    for (int k = 0; k < kBlocks; ++k) count += __popcll(__ballot(x[k] <= i));
+  }
+  return static_cast<int32_t>(count) - 1;
+}
+
+// Page and slot of token i, or false when any index is out of range.
+template <bool FUSED>
+__device__ __forceinline__ bool locate(const AppendParams& p, uint32_t i, uint32_t* page, uint32_t* slot) {
+  int32_t b;
+  int32_t pos;
+  if (FUSED) {
+    b = request_of(p, static_cast<int32_t>(i));
+    if (b < 0) return false;
+    const int32_t a0 = p.append_indptr[b], a1 = p.append_indptr[b + 1];
+    if (static_cast<int32_t>(i) >= a1) return false;
+    const int32_t pages = p.kv_indptr[b + 1] - p.kv_indptr[b];
+    const int32_t seq_len = (pages > 1 ? pages - 1 : 0) * static_cast<int32_t>(p.page_size) + p.kv_last_page_len[b];
+    pos = seq_len - (a1 - a0) + (static_cast<int32_t>(i) - a0);
+  } else {
+    b = p.batch_indices[i];
+    pos = p.positions[i];
+    if (b < 0 || static_cast<uint32_t>(b) >= p.batch_size) return false;
+  }
+  if (pos < 0) return false;
+  const int64_t first = p.kv_indptr[b];
+  const int64_t last = p.kv_indptr[b + 1];
+  const int64_t it = first + pos / static_cast<int32_t>(p.page_size);
+  if (first < 0 || it >= last || it >= p.num_indices) return false;
+  *page = static_cast<uint32_t>(p.kv_indices[it]);
+  if (*page >= p.num_pages) return false;
+  *slot = static_cast<uint32_t>(pos) % p.page_size;
+  return true;
+}
+
+// V: vectors per lane (the row, or its chunk, is V * 64 vectors); GUARD: the
+// row is not a multiple of that; MULTI: rows longer than one chunk.
+template <int V, bool GUARD, bool MULTI, bool FUSED>
 __global__ __launch_bounds__(kThreads) void append_kernel(const AppendParams p) {
   const uint32_t item = blockIdx.x;
   if (item >= p.total_items) return;
-  const uint32_t per_token = 2 * p.chunks_per_row;
-  const uint32_t i = item / per_token;
-  const uint32_t rem = item - i * per_token;
-  const uint32_t kv = rem / p.chunks_per_row;
-  const uint32_t chunk = rem - kv * p.chunks_per_row;
-  const uint32_t b = static_cast<uint32_t>(p.batch_indices[i]);
-  const int32_t pos = p.positions[i];
-  bool ok = b < p.batch_size && pos >= 0;
-  uint32_t page = 0;
-  if (ok) {
-    const int64_t first = p.kv_indptr[b];
-    const int64_t last = p.kv_indptr[b + 1];
-    const int64_t it = first + pos / static_cast<int32_t>(p.page_size);
-    ok = first >= 0 && it < last && it < p.num_indices;
-    if (ok) {
-      page = static_cast<uint32_t>(p.kv_indices[it]);
-      ok = page < p.num_pages;
-    }
+  uint32_t i, kv, chunk;
+  if (MULTI) {
+    const uint32_t per_token = 2 * p.chunks_per_row;
+    i = item / per_token;
+    const uint32_t rem = item - i * per_token;
+    kv = rem / p.chunks_per_row;
+    chunk = rem - kv * p.chunks_per_row;
+  } else {
+    i = item >> 1;
+    kv = item & 1;
+    chunk = 0;
   }
-  if (!ok) {
+  uint32_t page = 0, slot = 0;
+  if (!locate<FUSED>(p, i, &page, &slot)) {
     if (kv == 0 && chunk == 0 && threadIdx.x == 0 && p.err != nullptr) atomicAdd(p.err, 1);
     return;
   }
-  const uint32_t vec = chunk * kThreads + threadIdx.x;
-  if (GUARD && vec >= p.row_vecs) return;
-  const uint32_t slot = static_cast<uint32_t>(pos) % p.page_size;
-  const char* src = (kv ? p.value : p.key) + static_cast<int64_t>(i) * p.token_stride;
+  const u32x4* src = reinterpret_cast<const u32x4*>((kv ? p.value : p.key) + static_cast<int64_t>(i) * p.token_stride);
   const int64_t page_bytes = 2 * static_cast<int64_t>(p.page_size) * p.row_bytes;
-  char* dst = p.cache + static_cast<int64_t>(page) * page_bytes +
-              (static_cast<int64_t>(kv) * p.page_size + slot) * p.row_bytes;
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + vec);
-  // A plain nontemporal store: unlike the page copy, the append measured
-  // slower with the device-scope write-through store (prefill 16 x 1024
-  // tokens 25.3 us against 23.9-24.7 us per launch, decode 2.37 against 2.22).
-  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst) + vec);
+  u32x4* dst = reinterpret_cast<u32x4*>(p.cache + static_cast<int64_t>(page) * page_bytes +
+                                        (static_cast<int64_t>(kv) * p.page_size + slot) * p.row_bytes);
+  const uint32_t first_vec = chunk * (V * kThreads) + threadIdx.x;
+  u32x4 v[V];
+#pragma unroll
+  for (int c = 0; c < V; ++c) {
+    const uint32_t vec = first_vec + c * kThreads;
+    if (!GUARD || vec < p.row_vecs) v[c] = __builtin_nontemporal_load(src + vec);
+  }
+#pragma unroll
+  for (int c = 0; c < V; ++c) {
+    const uint32_t vec = first_vec + c * kThreads;
+    if (!GUARD || vec < p.row_vecs) store_row_vec(dst + vec, v[c]);
+  }
 }
 
 // One thread per appended token: finds its request by binary search over
@@ -113,6 +181,70 @@ __global__ __launch_bounds__(256) void positions_kernel(const int32_t* __restric
 }  // namespace
 }  // namespace pace_kv
 
+namespace pace_kv {
+namespace {
+
+template <int V, bool GUARD, bool MULTI, bool FUSED>
+const void* kernel_of() {
+  return reinterpret_cast<const void*>(&append_kernel<V, GUARD, MULTI, FUSED>);
+}
+
+template <bool FUSED>
+const void* pick_kernel(int v, bool guard, bool multi) {
+  switch (v) {
+    case 1: return guard ? kernel_of<1, true, false, FUSED>() : kernel_of<1, false, false, FUSED>();
+    case 2: return guard ? kernel_of<2, true, false, FUSED>() : kernel_of<2, false, false, FUSED>();
+    case 4: return guard ? kernel_of<4, true, false, FUSED>() : kernel_of<4, false, false, FUSED>();
+    case 8: return guard ? kernel_of<8, true, false, FUSED>() : kernel_of<8, false, false, FUSED>();
+    default:
+      if (multi) return guard ? kernel_of<16, true, true, FUSED>() : kernel_of<16, false, true, FUSED>();
+      return guard ? kernel_of<16, true, false, FUSED>() : kernel_of<16, false, false, FUSED>();
+  }
+}
+
+// Checks the arguments both forms share, sizes the grid and launches.
+int launch_append(AppendParams& p, int64_t nnz, int batch_size, int64_t num_pages, int64_t num_indices,
+                  int page_size, int64_t token_stride_bytes, int64_t row_bytes, bool fused, hipStream_t stream) {
+  if (nnz < 0 || batch_size < 0 || num_pages < 0 || num_indices < 0)
+    return fail(PACE_KV_EINVAL, "append: negative size");
+  if (nnz == 0) return PACE_KV_OK;
+  if (!p.key || !p.value || !p.cache || !p.kv_indices || !p.kv_indptr)
+    return fail(PACE_KV_EINVAL, "append: NULL argument");
+  if (page_size <= 0) return fail(PACE_KV_EINVAL, "append: page_size must be >= 1");
+  if (row_bytes <= 0 || row_bytes % kVecBytes != 0)
+    return fail(PACE_KV_EINVAL, "append: row bytes (H*D*elem) must be a positive multiple of 16");
+  if (token_stride_bytes < row_bytes || token_stride_bytes % kVecBytes != 0)
+    return fail(PACE_KV_EINVAL, "append: token stride must be >= row bytes and a multiple of 16");
+  if ((reinterpret_cast<uintptr_t>(p.key) | reinterpret_cast<uintptr_t>(p.value) |
+       reinterpret_cast<uintptr_t>(p.cache)) & 15u)
+    return fail(PACE_KV_EINVAL, "append: keys, values and cache must be 16-byte aligned");
+  if (num_pages > INT32_MAX) return fail(PACE_KV_ERANGE, "append: too many pages");
+  const int64_t row_vecs = row_bytes / kVecBytes;
+  const int64_t per_lane = (row_vecs + kThreads - 1) / kThreads;
+  int v = 1;
+  while (v < per_lane && v < kMaxVecsPerLane) v *= 2;
+  const int64_t chunk_vecs = static_cast<int64_t>(v) * kThreads;
+  const int64_t chunks = (row_vecs + chunk_vecs - 1) / chunk_vecs;
+  if (nnz > INT32_MAX || nnz * 2 * chunks >= (int64_t(1) << 25))
+    return fail(PACE_KV_ERANGE, "append: too many tokens for one launch (%lld)", (long long)nnz);
+  p.token_stride = token_stride_bytes;
+  p.num_indices = num_indices;
+  p.row_bytes = row_bytes;
+  p.batch_size = static_cast<uint32_t>(batch_size);
+  p.num_pages = static_cast<uint32_t>(num_pages);
+  p.page_size = static_cast<uint32_t>(page_size);
+  p.chunks_per_row = static_cast<uint32_t>(chunks);
+  p.total_items = static_cast<uint32_t>(nnz * 2 * chunks);
+  p.row_vecs = static_cast<uint32_t>(row_vecs);
+  const bool guard = row_vecs % chunk_vecs != 0;
+  const void* fn = fused ? pick_kernel<true>(v, guard, chunks > 1) : pick_kernel<false>(v, guard, chunks > 1);
+  void* args[] = {&p};
+  return hip_status(hipLaunchKernel(fn, dim3(p.total_items), dim3(kThreads), args, 0, stream), "append launch");
+}
+
+}  // namespace
+}  // namespace pace_kv
+
 using pace_kv::fail;
 using pace_kv::hip_status;
 
@@ -123,55 +255,43 @@ int pace_kv_append(const void* keys, const void* values, int64_t token_stride_by
                    void* cache, int64_t num_pages, const int32_t* kv_indices, int64_t num_indices,
                    const int32_t* kv_indptr, int page_size, int64_t row_bytes, int32_t* err_count,
                    void* stream) {
-  using namespace pace_kv;
-  if (nnz < 0 || batch_size < 0 || num_pages < 0 || num_indices < 0)
-    return fail(PACE_KV_EINVAL, "append: negative size");
-  if (nnz == 0) return PACE_KV_OK;
-  if (!keys || !values || !batch_indices || !positions || !cache || !kv_indices || !kv_indptr)
-    return fail(PACE_KV_EINVAL, "append: NULL argument");
-  if (page_size <= 0) return fail(PACE_KV_EINVAL, "append: page_size must be >= 1");
-  if (row_bytes <= 0 || row_bytes % kVecBytes != 0)
-    return fail(PACE_KV_EINVAL, "append: row bytes (H*D*elem) must be a positive multiple of 16");
-  if (token_stride_bytes < row_bytes || token_stride_bytes % kVecBytes != 0)
-    return fail(PACE_KV_EINVAL, "append: token stride must be >= row bytes and a multiple of 16");
-  if ((reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(values) |
-       reinterpret_cast<uintptr_t>(cache)) & 15u)
-    return fail(PACE_KV_EINVAL, "append: keys, values and cache must be 16-byte aligned");
-  if (num_pages > INT32_MAX) return fail(PACE_KV_ERANGE, "append: too many pages");
-  const int64_t chunks = (row_bytes + kRowBytes - 1) / kRowBytes;
-  if (nnz * 2 * chunks >= (int64_t(1) << 25))
-    return fail(PACE_KV_ERANGE, "append: too many tokens for one launch (%lld)", (long long)nnz);
-  AppendParams p;
+  if (nnz > 0 && (!batch_indices || !positions)) return fail(PACE_KV_EINVAL, "append: NULL argument");
+  pace_kv::AppendParams p = {};
   p.key = static_cast<const char*>(keys);
   p.value = static_cast<const char*>(values);
-  p.token_stride = token_stride_bytes;
   p.batch_indices = batch_indices;
   p.positions = positions;
   p.kv_indices = kv_indices;
   p.kv_indptr = kv_indptr;
-  p.num_indices = num_indices;
   p.cache = static_cast<char*>(cache);
   p.err = err_count;
-  p.row_bytes = row_bytes;
-  p.batch_size = static_cast<uint32_t>(batch_size);
-  p.num_pages = static_cast<uint32_t>(num_pages);
-  p.page_size = static_cast<uint32_t>(page_size);
-  p.chunks_per_row = static_cast<uint32_t>(chunks);
-  p.total_items = static_cast<uint32_t>(nnz * 2 * chunks);
-  p.row_vecs = static_cast<uint32_t>(row_bytes / kVecBytes);
-  void* args[] = {&p};
-  const bool guard = row_bytes % kRowBytes != 0;
-  const void* fn = guard ? reinterpret_cast<const void*>(&append_kernel<true>)
-                         : reinterpret_cast<const void*>(&append_kernel<false>);
-  return hip_status(hipLaunchKernel(fn, dim3(p.total_items), dim3(kThreads), args, 0,
-                                    static_cast<hipStream_t>(stream)),
-                    "append launch");
+  return pace_kv::launch_append(p, nnz, batch_size, num_pages, num_indices, page_size, token_stride_bytes,
+                                row_bytes, false, static_cast<hipStream_t>(stream));
+}
+
+int pace_kv_append_indptr(const void* keys, const void* values, int64_t token_stride_bytes, int64_t nnz,
+                          const int32_t* append_indptr, int batch_size, void* cache, int64_t num_pages,
+                          const int32_t* kv_indices, int64_t num_indices, const int32_t* kv_indptr,
+                          const int32_t* kv_last_page_len, int page_size, int64_t row_bytes,
+                          int32_t* err_count, void* stream) {
+  if (nnz > 0 && batch_size == 0) return fail(PACE_KV_EINVAL, "append: tokens without requests");
+  if (nnz > 0 && (!append_indptr || !kv_last_page_len)) return fail(PACE_KV_EINVAL, "append: NULL argument");
+  pace_kv::AppendParams p = {};
+  p.key = static_cast<const char*>(keys);
+  p.value = static_cast<const char*>(values);
+  p.append_indptr = append_indptr;
+  p.kv_last_page_len = kv_last_page_len;
+  p.kv_indices = kv_indices;
+  p.kv_indptr = kv_indptr;
+  p.cache = static_cast<char*>(cache);
+  p.err = err_count;
+  return pace_kv::launch_append(p, nnz, batch_size, num_pages, num_indices, page_size, token_stride_bytes,
+                                row_bytes, true, static_cast<hipStream_t>(stream));
 }
 
 int pace_kv_batch_indices_positions(const int32_t* append_indptr, const int32_t* seq_lens,
                                     int batch_size, int64_t nnz, int32_t* batch_indices,
                                     int32_t* positions, void* stream) {
-  using namespace pace_kv;
   if (nnz < 0 || batch_size < 0) return fail(PACE_KV_EINVAL, "positions: negative size");
   if (nnz == 0) return PACE_KV_OK;
   if (batch_size == 0) return fail(PACE_KV_EINVAL, "positions: tokens without requests");
@@ -183,7 +303,7 @@ int pace_kv_batch_indices_positions(const int32_t* append_indptr, const int32_t*
   const uint32_t blocks = (n + 255) / 256;
   void* args[] = {const_cast<int32_t**>(&append_indptr), const_cast<int32_t**>(&seq_lens), &bs, &n,
                   &batch_indices, &positions};
-  return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(&positions_kernel), dim3(blocks),
+  return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(&pace_kv::positions_kernel), dim3(blocks),
                                     dim3(256), args, 0, static_cast<hipStream_t>(stream)),
                     "positions launch");
 }

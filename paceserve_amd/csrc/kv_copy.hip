@@ -82,10 +82,16 @@ __device__ __forceinline__ uint32_t page_of(const int32_t* ids, uint32_t j) {
 // Measured on MI355X against plain (launches <= 1 GiB) or nontemporal pack
 // stores and nontemporal unpack stores, pack+unpack runs 0.8% (16 GiB of
 // 256 KiB pages) to 5.9% (64 MiB) faster, and a fused move 0.5% to 4.2%.
+// A store of more than 64 bits reads its data registers after it issues, so
+// the next instructions must not overwrite them; the compiler inserts those
+// wait states for the stores it emits itself but cannot for one written as
+// asm, so the asm carries them (s_nop 1: two wait states).  Without them a
+// variant that computed its next address into the stored registers wrote
+// wrong data.
 template <bool PACK>
 __device__ __forceinline__ void store_vec(const u32x4 v, u32x4* d) {
-  if (PACK) asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(d), "v"(v) : "memory");
-  else asm volatile("global_store_dwordx4 %0, %1, off nt sc1" : : "v"(d), "v"(v) : "memory");
+  if (PACK) asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" : : "v"(d), "v"(v) : "memory");
+  else asm volatile("global_store_dwordx4 %0, %1, off nt sc1\n\ts_nop 1" : : "v"(d), "v"(v) : "memory");
 }
 
 // The copy of one 1 KiB row: item blockIdx.x (page j, row r of it) of layer

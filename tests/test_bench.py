@@ -123,3 +123,21 @@ def test_summarize_promote_splits_the_inline_kernels(tmp_path):
     assert "| unpack (destination ids inline) | 3 | 152.0 | 152.0 |" in md
     assert "| move (both inline) | 2 | 165.0 | 165.0 |" in md
     assert "of which 302.0 us are the two kernels" in md and "of which 165.0 us is the move kernel" in md
+
+
+def test_summarize_kernel_pmc_groups_by_kernel_and_grid(tmp_path):
+    app = "void pace_kv::(anonymous namespace)::append_kernel<2, false, false, true>(pace_kv::(anonymous namespace)::AppendParams)"
+    rows = []
+    for i, (grid, val) in enumerate([(2097152, 100.0), (2097152, 300.0), (32768, 7.0)]):
+        rows.append({"Dispatch_Id": i + 1, "Kernel_Name": app, "Grid_Size": grid, "Counter_Name": "FETCH_SIZE",
+                     "Counter_Value": val})
+    rows.append({"Dispatch_Id": 9, "Kernel_Name": "other", "Grid_Size": 64, "Counter_Name": "FETCH_SIZE",
+                 "Counter_Value": 1.0})
+    a = write_csv(tmp_path / "a.csv", rows)
+    b = write_csv(tmp_path / "b.csv", [dict(r, Counter_Name="WRITE_SIZE", Counter_Value=2 * r["Counter_Value"])
+                                       for r in rows])
+    md = bench.summarize_kernel_pmc("append_kernel", "CMD1\nCMD2", [a, b])
+    assert "CMD1\nCMD2" in md
+    assert "| append_kernel<2, false, false, true> | 32768 | 1 | 7 | 14 |" in md
+    assert "| append_kernel<2, false, false, true> | 2097152 | 2 | 200 | 400 |" in md
+    assert "other" not in md

@@ -1,5 +1,6 @@
-"""Paged append on the HIP path (pace_kv_append, pace_kv_batch_indices_positions)
-against the reference's FlashInfer example and the oracle, and the producer ->
+"""Paged append on the HIP path (pace_kv_append, pace_kv_batch_indices_positions,
+and pace_kv_append_indptr, which derives positions in the same launch) against
+the reference's FlashInfer example and the oracle, and the producer ->
 migration -> producer sequence a partially prefilled promotion needs."""
 import numpy as np
 import pytest
@@ -37,17 +38,29 @@ def test_flashinfer_example_known_answer(gpu):
     ap.append_paged_kv_cache(kk, vv, bi, pos, cache, kv_indices, kv_indptr, last)
     torch.cuda.synchronize()
     assert np.array_equal(words(cache).cpu().numpy().astype(np.uint16), want)
+    fused = torch.zeros_like(cache)
+    ap.append_paged_kv_cache_indptr(kk, vv, i32([0, 3, 10], gpu), fused, kv_indices, kv_indptr, last)
+    torch.cuda.synchronize()
+    assert np.array_equal(words(fused).cpu().numpy().astype(np.uint16), want)
 
 
-@pytest.mark.parametrize("dtype,H,D,P", [
-    (torch.bfloat16, 8, 128, 16), (torch.float16, 32, 128, 16), (torch.float16, 1, 64, 4),
-    (torch.float32, 4, 64, 16), (torch.float8_e4m3fn, 8, 128, 16), (torch.bfloat16, 2, 8, 16)])
-def test_mixed_prefill_and_decode_batch_matches_oracle(gpu, dtype, H, D, P):
-    rng = np.random.default_rng(H * D + P)
-    R = 6
+# Rows of 2 KiB (two vectors per lane), 8 KiB (eight), 128 B and 32 B (part of
+# one lane set), 1 KiB, 10 KiB (sixteen, guarded), 32 KiB and 24 KiB (two
+# chunks of 16 KiB, the second guarded); R requests, more than one wave's 64
+# for the fused form's request search.
+@pytest.mark.parametrize("dtype,H,D,P,R", [
+    (torch.bfloat16, 8, 128, 16, 6), (torch.float16, 32, 128, 16, 6), (torch.float16, 1, 64, 4, 6),
+    (torch.float32, 4, 64, 16, 6), (torch.float8_e4m3fn, 8, 128, 16, 6), (torch.bfloat16, 2, 8, 16, 6),
+    (torch.float16, 40, 128, 16, 5), (torch.bfloat16, 64, 256, 16, 4), (torch.bfloat16, 96, 128, 16, 3),
+    (torch.bfloat16, 8, 128, 16, 130)])
+def test_mixed_prefill_and_decode_batch_matches_oracle(gpu, dtype, H, D, P, R):
+    print(f"append case {dtype} H={H} D={D} P={P} R={R}", flush=True)
+    rng = np.random.default_rng(H * D + P + R)
     prior = rng.integers(0, 40, R)                 # tokens already in each request
     app = rng.integers(1, 25, R)                   # tokens appended now
     app[::2] = 1                                   # decode requests append one token
+    if R > 6:
+        app[3::7] = 0                              # requests appending nothing
     total = prior + app
     pages = -(-total // P)
     NP = int(pages.sum()) + 5
@@ -66,11 +79,17 @@ def test_mixed_prefill_and_decode_batch_matches_oracle(gpu, dtype, H, D, P):
         words(k).cpu().numpy(), words(v).cpu().numpy(),
         *orc.get_batch_indices_positions(append_indptr, orc.get_seq_lens(kv_indptr, last, P), nnz),
         words(cache).cpu().numpy(), kv_indices, kv_indptr, P)
+    fused = cache.clone()
     seq = ap.get_seq_lens(i32(kv_indptr, gpu), i32(last, gpu), P)
     bi, pos = ap.get_batch_indices_positions(i32(append_indptr, gpu), seq, nnz)
     ap.append_paged_kv_cache(k, v, bi, pos, cache, i32(kv_indices, gpu), i32(kv_indptr, gpu), i32(last, gpu))
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ap.append_paged_kv_cache_indptr(k, v, i32(append_indptr, gpu), fused, i32(kv_indices, gpu), i32(kv_indptr, gpu),
+                                    i32(last, gpu), err=err)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(words(cache).cpu().numpy(), want)
+    np.testing.assert_array_equal(words(fused).cpu().numpy(), want)
+    assert int(err.item()) == 0
 
 
 def test_out_of_range_tokens_are_skipped_and_counted(gpu):
@@ -84,6 +103,26 @@ def test_out_of_range_tokens_are_skipped_and_counted(gpu):
     torch.cuda.synchronize()
     assert int(err.item()) == 3
     assert (cache[3, :, 1] == 1).all() and int((cache != 0).sum()) == 2 * 64
+
+
+def test_fused_append_skips_and_counts_tokens_out_of_range(gpu):
+    """Tokens past the last request's offsets, a request whose last-page
+    length puts its tokens before position 0, and a page id past the cache
+    are skipped and counted once per token; the other tokens land."""
+    cache = torch.zeros(4, 2, 4, 1, 64, dtype=torch.float16, device=gpu)
+    k = torch.ones(6, 1, 64, dtype=torch.float16, device=gpu)
+    # request 0: 2 tokens into page 3 (one page, last_len 2: positions 0, 1)
+    # request 1: 2 tokens with last_len 1 on one page -> positions -1, 0
+    # request 2: 1 token into page 9 (past the cache)
+    # tokens 5: beyond append_indptr[-1]
+    ai = i32([0, 2, 4, 5], gpu)
+    kv_indptr, kv_indices, last = i32([0, 1, 2, 3], gpu), i32([3, 1, 9], gpu), i32([2, 1, 1], gpu)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ap.append_paged_kv_cache_indptr(k, k, ai, cache, kv_indices, kv_indptr, last, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 3                    # request 1's first token, request 2's, token 5
+    assert (cache[3, :, :2] == 1).all() and (cache[1, :, 0] == 1).all()
+    assert int((cache != 0).sum()) == 3 * 2 * 64
 
 
 def test_partially_prefilled_request_promoted_then_continued(gpu):
