@@ -796,12 +796,29 @@ CPU_CONFIG_SECONDS = 3.0
 CPU_CONFIG_LAYERS = 4
 
 
-def run_config(args, name: str, dev) -> dict:
+def run_staging_leg(args, name: str, dev) -> dict:
+    """The pinned-host legs of a workload (run_staging) on its own pools,
+    then the exact check of both pools (the round trip writes the same
+    destination pages as the device path)."""
+    from paceserve_amd import workloads
+
+    w = workloads.get(name)
+    log(f"staging {w.name}: {w.description}")
+    src, dst, plan, s_ids, d_ids = device_setup(w, dev)
+    st = run_staging(w, dev, src, dst, s_ids, d_ids)
+    st["workload"] = w.name
+    if args.verify:
+        st["verified"] = verify(w, src, dst, s_ids, d_ids, dev)
+        log(f"staging {w.name}: verified {st['verified']}")
+    return st
+
+
+def run_config(args, name: str, dev, staging: dict = None) -> dict:
     """One of the other workloads, measured in the same process after the
     headline: K timed steps of pack + unpack (value and roofline as for the
-    headline), the exact check of both pools, the pinned-host legs when the
-    workload has them (checked again after), the identity-id copy ceiling
-    (last: it writes pages no id names) and a short CPU sample."""
+    headline), the exact check of both pools, the identity-id copy ceiling
+    (last: it writes pages no id names) and a short CPU sample.  `staging`:
+    the workload's pinned-host legs, measured before the headline."""
     import argparse
 
     from paceserve_amd import workloads
@@ -821,15 +838,8 @@ def run_config(args, name: str, dev) -> dict:
     if args.verify:
         out["verified"] = verify(w, src, dst, s_ids, d_ids, dev)
         log(f"config {w.name}: verified {out['verified']}")
-    if not args.no_staging and w.staging in ("pinned", "both"):
-        settle = link_settle(dev)
-        st = run_staging(w, dev, src, dst, s_ids, d_ids)
-        st["link_probe"] = settle
-        st["workload"] = w.name
-        out["staging"] = st
-        if args.verify:
-            out["verified_after_staging"] = verify(w, src, dst, s_ids, d_ids, dev)
-            log(f"config {w.name}: verified after staging {out['verified_after_staging']}")
+    if staging is not None:
+        out["staging"] = staging
     out["copy_ceiling"] = run_ceiling(w, dev, src, dst, plan.n_pages)
     if not args.no_cpu:
         layers = min(CPU_CONFIG_LAYERS, cpu_sample_layers(w))
@@ -1331,6 +1341,37 @@ def main():
     _native.load()
     dev = torch.device("cuda", 0)
     w = workloads.get(args.workload)
+    # Host-link legs first, in a process that has run no other GPU work yet.
+    # How the runtime carries a stream's copies (DMA engine or blit kernel)
+    # depends on the process's earlier GPU work: after some sequences of graph
+    # captures and small copies, the same pinned round trip ran at 26-28 GB/s
+    # per direction instead of 45-48, with the device-to-host copies carried
+    # by blit kernels.  Device legs are not affected.
+    staging_names = []
+    if not args.no_staging:
+        if args.staging or w.staging in ("pinned", "both"):
+            staging_names.append(w.name)
+        if not args.no_configs:
+            staging_names += [n for n in workloads.NAMES
+                              if n != w.name and workloads.get(n).staging in ("pinned", "both")]
+    promote = None
+    early_staging = {}
+    if staging_names or not args.no_promote:
+        settle = link_settle(dev)
+        log(f"host link settled after {settle['waited_s']} s at {settle['d2h_gbs']} GB/s D2H")
+        if not args.no_promote:
+            promote = run_promote(dev)
+            promote["link_probe"] = settle
+        for name in staging_names:
+            early_staging[name] = run_staging_leg(args, name, dev)
+            early_staging[name]["link_probe"] = settle
+    if early_staging:
+        # The staging pools go back to the driver, which scrubs them with the
+        # DMA engines and HBM bandwidth: the headline waits until a D2H probe
+        # runs at the link's rate again.
+        torch.cuda.empty_cache()
+        after = link_settle(dev)
+        log(f"after the staging legs: link settled after {after['waited_s']} s at {after['d2h_gbs']} GB/s D2H")
     log(f"workload {w.name}: {w.description}")
     src, dst, plan, s_ids, d_ids = device_setup(w, dev)
     res = run_device(args, w, dev, src, dst, plan, s_ids, d_ids)
@@ -1347,23 +1388,7 @@ def main():
         log(f"CPU baseline on {os.cpu_count()} cores, {layers} layers ...")
         cpu = run_cpu_baseline(w, layers, src, dst, plan)
         log(f"CPU baseline: {cpu['value']} GB/s")
-    # Host-link legs run while the workload's pools are still allocated: large
-    # frees make the driver scrub memory with the same DMA engines.
-    staging = None
-    promote = None
-    want_staging = not args.no_staging and (args.staging or w.staging in ("pinned", "both"))
-    if want_staging or not args.no_promote:
-        settle = link_settle(dev)
-        log(f"host link settled after {settle['waited_s']} s at {settle['d2h_gbs']} GB/s D2H")
-        if want_staging:
-            staging = run_staging(w, dev, src, dst, s_ids, d_ids)
-            staging["link_probe"] = settle
-            staging["workload"] = w.name
-            if args.verify:
-                res["verified_after_staging"] = verify(w, src, dst, s_ids, d_ids, dev)
-        if not args.no_promote:
-            promote = run_promote(dev)
-            promote["link_probe"] = settle
+    staging = early_staging.get(w.name)
     # The identity-id ceiling writes destination pages that no id names, so it
     # runs after every check of the pools; the calibration copies come last.
     ceiling = run_ceiling(w, dev, src, dst, plan.n_pages) if args.mode == "buffer" else None
@@ -1371,13 +1396,11 @@ def main():
         run_calibration(dev)
     dropin = None
     if not args.no_dropin:
-        settle = link_settle(dev)       # the promote leg has just freed its pools
+        settle = link_settle(dev)
         dropin = run_dropin(dev)
         dropin["link_probe"] = settle
     # Memory freed from here on stays in torch's cache for the later legs and
-    # workloads (no empty_cache): memory returned to the driver is scrubbed
-    # with the DMA engines the host legs use, which halved the staging rates
-    # of workloads measured after a freed 215 GB pool pair.
+    # workloads (no empty_cache), so the driver scrubs nothing while they run.
     del src, dst, s_ids, d_ids
     channel = None
     if not args.no_channel:
@@ -1386,9 +1409,10 @@ def main():
         channel["link_probe"] = settle
     configs = None
     if not args.no_configs:
-        configs = {name: run_config(args, name, dev) for name in workloads.NAMES if name != w.name}
-    if staging is None and configs:
-        staging = next((c["staging"] for c in configs.values() if "staging" in c), None)
+        configs = {name: run_config(args, name, dev, early_staging.get(name))
+                   for name in workloads.NAMES if name != w.name}
+    if staging is None and early_staging:
+        staging = next(iter(early_staging.values()))
 
     line = {
         "metric": METRIC,
@@ -1424,9 +1448,8 @@ def main():
     if tr is not None:
         line["roofline"]["traffic"] = tr["traffic_bytes_per_launch"]
         line["roofline"]["traffic_source"] = f"profiles/page_copy_{w.name}_traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)"
-    for key in ("verified", "verified_after_staging"):
-        if key in res:
-            line[key] = res[key]
+    if "verified" in res:
+        line["verified"] = res["verified"]
     if "verified" in res:
         line["verified_what"] = VERIFIED_WHAT
     if configs:
