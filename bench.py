@@ -1053,12 +1053,39 @@ def summarize_pmc(fetch_csv: str, write_csv: str, workload: str) -> dict:
     return out
 
 
+def requests_per_launch(rdreq_csv: str, wrreq_csv: str) -> dict:
+    """HBM bytes per page-copy launch from request counts, with no scale
+    factor: TCC read requests are 128 bytes unless counted as 32-byte ones
+    (TCC_EA0_RDREQ_sum, TCC_EA0_RDREQ_32B_sum), write requests 64 bytes
+    unless 32 (TCC_EA0_WRREQ_sum, TCC_EA0_WRREQ_64B_sum); TCC_BUBBLE_sum is
+    reported beside them (0 here: the 128-byte reads it would count are the
+    ones FETCH_SIZE weighs at 64 bytes)."""
+    def mean(path, counter):
+        vals = [v for k, vs in _per_dispatch(path, counter).items() if "page_copy_kernel" in k for v in vs]
+        return statistics.mean(vals) if vals else 0.0
+
+    rd, rd32, bubble = (mean(rdreq_csv, c) for c in ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_BUBBLE_sum"))
+    wr, wr64 = mean(wrreq_csv, "TCC_EA0_WRREQ_sum"), mean(wrreq_csv, "TCC_EA0_WRREQ_64B_sum")
+    read = (rd - rd32) * 128 + rd32 * 32
+    write = wr64 * 64 + (wr - wr64) * 32
+    return {"rdreq": rd, "rdreq_32b": rd32, "bubble": bubble, "wrreq": wr, "wrreq_64b": wr64,
+            "read_bytes_per_launch": int(read), "write_bytes_per_launch": int(write),
+            "bytes_per_launch": int(read + write), "rdreq_csv": rdreq_csv, "wrreq_csv": wrreq_csv}
+
+
 def timed_dispatches(trace_csv: str, bench: dict):
     """The page-copy dispatches of the timed steps in a rocprofv3 kernel
-    trace of one bench.py run: page-copy launches in dispatch order are the
-    W warm-up steps, then the K timed steps, then the launch-timing pass and
-    the copy-ceiling run; returns (durations ns, span ns) of the timed ones."""
-    rows = [r for r in _rows(trace_csv) if "page_copy_kernel" in r["Kernel_Name"]]
+    trace of one bench.py run.  The headline's launches are the page-copy
+    dispatches whose grid covers its batch (64 threads per 1 KiB row of each
+    of its pages; the staging legs that run earlier and the other workloads
+    that run later have other batches); in dispatch order they are the W
+    warm-up steps, then the K timed steps, then the launch-timing pass and
+    the copy ceiling.  Returns (durations ns, span ns) of the timed ones."""
+    cfg = bench["config"]
+    page_bytes = cfg["payload_bytes"] // (cfg["layers"] * cfg["pages"])
+    grid_x = -(-page_bytes // 1024) * cfg["pages"] * 64
+    rows = [r for r in _rows(trace_csv) if "page_copy_kernel" in r["Kernel_Name"]
+            and int(r.get("Grid_Size_X", grid_x)) == grid_x]
     rows.sort(key=lambda r: int(r["Dispatch_Id"]))
     per_step = bench["roofline"]["launches_per_step"]
     first = bench["warmup"] * per_step
@@ -1103,8 +1130,8 @@ def summarize_stats(stats_csv: str, bench_json: str, command: str, trace_csv: st
         out += ["", f"bench.py in the same run (HIP events on the launch stream): mean launch "
                 f"{rf['mean_launch_us']} us, achieved {rf['achieved']} GB/s ({rf['frac'] * 100:.1f}% of 8 TB/s); "
                 f"headline value {bench['value']} GB/s.",
-                f"rocprofv3 average over all {calls} page-copy launches of the run (warm-up, timed steps, "
-                f"launch-timing pass, copy ceiling) {avg_us:.2f} us."]
+                f"rocprofv3 average over all {calls} page-copy launches of the run (every leg and workload it "
+                f"ran, of every size) {avg_us:.2f} us; the headline's own launches are the line below."]
         if trace_csv:
             durs, span = timed_dispatches(trace_csv, bench)
             mean_us = statistics.mean(durs) / 1e3
@@ -1252,12 +1279,14 @@ def pmc_markdown(traffic_json: str) -> str:
     # <dir>/w_counter_collection.csv) where the summary read them
     fdir = os.path.dirname(t.get("fetch_csv", f"pmc_fetch_{wl}/f_counter_collection.csv"))
     wdir = os.path.dirname(t.get("write_csv", f"pmc_write_{wl}/w_counter_collection.csv"))
+    rq = t.get("requests")
+    extra = f" {rq['rdreq_csv']} {rq['wrreq_csv']}" if rq else ""
     cmds = [
         "export TMPDIR=/tmp",
-        f"timeout -s KILL 300 rocprofv3 --pmc FETCH_SIZE --output-format csv -d {fdir} -o f -- {run}",
-        f"timeout -s KILL 300 rocprofv3 --pmc WRITE_SIZE --output-format csv -d {wdir} -o w -- {run}",
+        f"timeout -s KILL 240 rocprofv3 --pmc FETCH_SIZE --output-format csv -d {fdir} -o f -- {run}",
+        f"timeout -s KILL 240 rocprofv3 --pmc WRITE_SIZE --output-format csv -d {wdir} -o w -- {run}",
         f"python3 bench.py --summarize-pmc {fdir}/f_counter_collection.csv "
-        f"{wdir}/w_counter_collection.csv {wl} > profiles/page_copy_{wl}_traffic.json",
+        f"{wdir}/w_counter_collection.csv {wl}{extra} > profiles/page_copy_{wl}_traffic.json",
         f"python3 bench.py --pmc-markdown profiles/page_copy_{wl}_traffic.json > profiles/page_copy_{wl}_traffic.md",
     ]
     out = [f"# {t['kernel']} on {wl} - HBM traffic per launch (rocprofv3 PMC)", "",
@@ -1275,6 +1304,24 @@ def pmc_markdown(traffic_json: str) -> str:
                 "read once and written once).",
                 f"Measured HBM traffic per launch: {t['traffic_bytes_per_launch']} B = "
                 f"{t['traffic_bytes_per_launch'] / alg:.5f} x algorithmic: no re-reads, no partial-line writes."]
+    if rq:
+        rdir = os.path.dirname(rq["rdreq_csv"])
+        qdir = os.path.dirname(rq["wrreq_csv"])
+        out += ["", "Cross-check from request counts, with no scale factor (two more passes of the same run, "
+                "made before the summary above):", "",
+                "```",
+                f"timeout -s KILL 240 rocprofv3 --pmc TCC_EA0_RDREQ_sum TCC_EA0_RDREQ_32B_sum TCC_BUBBLE_sum "
+                f"--output-format csv -d {rdir} -o r -- {run}",
+                f"timeout -s KILL 240 rocprofv3 --pmc TCC_EA0_WRREQ_sum TCC_EA0_WRREQ_64B_sum "
+                f"--output-format csv -d {qdir} -o q -- {run}",
+                "```", "",
+                f"- read requests per launch {rq['rdreq']:.0f} (32-byte: {rq['rdreq_32b']:.0f}; TCC_BUBBLE "
+                f"{rq['bubble']:.0f}) x 128 B = {rq['read_bytes_per_launch']} B;",
+                f"- write requests per launch {rq['wrreq']:.0f} (64-byte: {rq['wrreq_64b']:.0f}) x 64 B = "
+                f"{rq['write_bytes_per_launch']} B;",
+                f"- together {rq['bytes_per_launch']} B = {rq['bytes_per_launch'] / alg:.5f} x algorithmic. "
+                "FETCH_SIZE weighs the 128-byte read requests at 64 bytes (TCC_BUBBLE, which it uses to "
+                "count them, stays 0), hence the scale of 2 above."]
     out += ["(Counter collection serialises dispatches, so runs under --pmc report lower throughput; "
             "only the byte counts are used.)"]
     return "\n".join(out) + "\n"
@@ -1294,8 +1341,10 @@ def main():
         channel_sender(sys.argv[2])
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-pmc":
-        # python bench.py --summarize-pmc FETCH.csv WRITE.csv WORKLOAD
+        # python bench.py --summarize-pmc FETCH.csv WRITE.csv WORKLOAD [RDREQ.csv WRREQ.csv]
         d = summarize_pmc(sys.argv[2], sys.argv[3], sys.argv[4])
+        if len(sys.argv) > 6:
+            d["requests"] = requests_per_launch(sys.argv[5], sys.argv[6])
         print(json.dumps(d, indent=1))
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--pmc-markdown":

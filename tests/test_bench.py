@@ -81,16 +81,25 @@ def test_pmc_markdown_states_algorithmic_bytes_per_layer_chunk(tmp_path):
 
 
 def test_timed_dispatches_skip_warmup_and_later_passes(tmp_path):
-    # 2 warm-up steps and 3 timed steps of 2 launches, then 4 more launches
+    # 2 warm-up steps and 3 timed steps of 2 launches, then 4 more launches;
+    # page copies of another batch (a staging leg before, another workload
+    # after) have another grid and are skipped
+    cfg = {"pages": 10, "layers": 4, "payload_bytes": 4 * 10 * 65536}
+    grid = 64 * 10 * 64
     rows, t = [], 0
+    rows.append({"Dispatch_Id": 1, "Kernel_Name": COPY, "Start_Timestamp": 0, "End_Timestamp": 3,
+                 "Grid_Size_X": 7 * 64})
     for i in range(2 * 2 + 3 * 2 + 4):
         dur = 10 if 4 <= i < 10 else 99
-        rows.append({"Dispatch_Id": i + 1, "Kernel_Name": COPY, "Start_Timestamp": t,
-                     "End_Timestamp": t + dur})
+        rows.append({"Dispatch_Id": i + 2, "Kernel_Name": COPY, "Start_Timestamp": t,
+                     "End_Timestamp": t + dur, "Grid_Size_X": grid})
         t += dur + 1
-    rows.insert(3, {"Dispatch_Id": 100, "Kernel_Name": "other", "Start_Timestamp": 0, "End_Timestamp": 5})
+    rows.insert(3, {"Dispatch_Id": 100, "Kernel_Name": "other", "Start_Timestamp": 0, "End_Timestamp": 5,
+                    "Grid_Size_X": grid})
+    rows.append({"Dispatch_Id": 200, "Kernel_Name": COPY, "Start_Timestamp": t, "End_Timestamp": t + 1,
+                 "Grid_Size_X": 3 * 64})
     path = write_csv(tmp_path / "k.csv", rows)
-    b = {"warmup": 2, "steps": 3, "roofline": {"launches_per_step": 2}}
+    b = {"warmup": 2, "steps": 3, "roofline": {"launches_per_step": 2}, "config": cfg}
     durs, span = bench.timed_dispatches(path, b)
     assert durs == [10] * 6
     assert span == 6 * 10 + 5
