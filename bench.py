@@ -834,6 +834,11 @@ def run_config(args, name: str, dev, staging: dict = None) -> dict:
            "frac_of_hbm_peak": round(res["value"] / HBM_PEAK_GBS, 4), "steps": sub.steps, "warmup": args.warmup,
            "ms_per_step": round(res["event_ms_per_step"], 4), "pack_ms": res["pack_ms_mean"],
            "unpack_ms": res["unpack_ms_mean"], "roofline": res["roofline"]}
+    tr = traffic_from_profiles(w.name)
+    if tr is not None:
+        out["roofline"]["traffic"] = tr["traffic_bytes_per_launch"]
+        out["roofline"]["traffic_source"] = (f"profiles/page_copy_{w.name}_traffic.json "
+                                             "(rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)")
     log(f"config {w.name}: {out['value']} GB/s ({out['frac_of_hbm_peak'] * 100:.1f}% of peak), K={sub.steps}")
     if args.verify:
         out["verified"] = verify(w, src, dst, s_ids, d_ids, dev)
