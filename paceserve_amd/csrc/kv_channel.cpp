@@ -785,6 +785,16 @@ int publish_dev_chunk(pace_kv_channel* ch, uint64_t id, int64_t c, const Chunkin
   return PACE_KV_OK;
 }
 
+// Sender: gives up a device message after packs into the ring may have been
+// enqueued.  An unpublished slot is reserved again by the next record at its
+// position, whose pack may run on another stream: the packs enqueued here
+// finish before this returns, so no late write lands in a slot that a later
+// message owns.
+int abandon_device(pace_kv_channel* ch, uint64_t id, int rc, hipStream_t stream) {
+  (void)hipStreamSynchronize(stream);
+  return abandon(ch, id, rc);
+}
+
 // Sender: packs every chunk straight into a device slot.  Chunk c is packed
 // before chunk c-1 is published, so the GPU has the next pack queued while
 // this thread waits for the previous one; at most one slot is reserved and
@@ -804,12 +814,12 @@ int send_device(pace_kv_channel* ch, const void* const* src_layers, int64_t pool
     }
     if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(ch->dev_packed[idx], stream), "channel send record");
     if (rc == PACE_KV_OK && c > 0) rc = publish_dev_chunk(ch, id, c - 1, k.at(c - 1), prev);
-    if (rc) return abandon(ch, id, rc);
+    if (rc) return abandon_device(ch, id, rc, stream);
     prev = idx;
   }
   if (k.num_chunks > 0) {
     const int rc = publish_dev_chunk(ch, id, k.num_chunks - 1, k.at(k.num_chunks - 1), prev);
-    if (rc) return abandon(ch, id, rc);
+    if (rc) return abandon_device(ch, id, rc, stream);
   }
   return PACE_KV_OK;
 }
@@ -840,7 +850,12 @@ int recv_device(pace_kv_channel* ch, void* const* dst_layers, int64_t pool_pages
     if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(ch->dev_unpacked[idx], stream), "channel recv record");
     if (rc == PACE_KV_OK)
       rc = hip_status(hipEventSynchronize(ch->dev_unpacked[idx]), "channel unpack out of the device ring");
-    if (rc) return fail_rx(ch, rc);
+    if (rc) {
+      // The slot goes back to the sender only after an unpack that was
+      // enqueued has stopped reading it.
+      (void)hipStreamSynchronize(stream);
+      return fail_rx(ch, rc);
+    }
     finish_chunk(ch);
   }
   return PACE_KV_OK;
