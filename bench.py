@@ -557,9 +557,12 @@ def run_dropin(dev, steps: int = 10, warmup: int = 2) -> dict:
 CHANNEL_SLOT_BYTES = 32 << 20
 CHANNEL_SLOTS = 4
 CHANNEL_THREADS = 4
-# The same-GPU device ring: 4 slots of 128 MiB (one 512 MiB allocation shared
-# between the two processes).
-CHANNEL_DEVICE_SLOT_BYTES = 128 << 20
+# The same-GPU device ring: 4 slots of 256 MiB (one 1 GiB allocation shared
+# between the two processes, the largest the library exports).  Measured on
+# the 4096-token request, from the pages' header to the last unpack: 329 us
+# with 256 MiB slots, 368 us with 128 MiB, 394 us with 8 x 64 MiB and 456 us
+# with 8 x 32 MiB: every chunk adds a pack, an unpack and a hand-over.
+CHANNEL_DEVICE_SLOT_BYTES = 256 << 20
 
 
 def channel_sender(name: str) -> None:

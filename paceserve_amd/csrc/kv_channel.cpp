@@ -390,6 +390,10 @@ struct pace_kv_channel {
   uint64_t rx_msg = 0;
   Chunking rx_chunks;
   int64_t rx_next = 0;
+  // Device receive: records read whose slots are not released yet (their
+  // unpacks are in flight), oldest first; the next record to read sits
+  // rx_held positions past `tail`.  Zero outside pace_kv_channel_recv.
+  uint32_t rx_held = 0;
   // this process's view of the device ring
   char* dev_ring = nullptr;
   int dev_device = -1;
@@ -457,7 +461,7 @@ void publish(pace_kv_channel* ch) {
 int next_record(pace_kv_channel* ch, int timeout_ms, uint32_t* idx, const char* what) {
   ChannelCtl* c = ch->ctl;
   take_role(c->receiver);
-  const uint32_t t = c->tail.load(std::memory_order_relaxed);
+  const uint32_t t = c->tail.load(std::memory_order_relaxed) + ch->rx_held;
   const uint64_t msg = ch->rx_msg;
   const bool active = ch->rx_active;
   PACE_KV_TRY(wait_for(ch, &c->head, c->sender,
@@ -824,39 +828,97 @@ int send_device(pace_kv_channel* ch, const void* const* src_layers, int64_t pool
   return PACE_KV_OK;
 }
 
-// Receiver: a device chunk whose read failed still releases its slot, and
-// the rest of its message is dropped by the next header receive.
+// Receiver: a device chunk whose copy to host memory failed still releases
+// its slot (the copy is synchronous), and the rest of its message is dropped
+// by the next header receive.
 int fail_rx(pace_kv_channel* ch, int rc) {
   ch->rx_active = false;
   release(ch);
   return rc;
 }
 
-// Receiver: unpacks every chunk straight out of its device slot and releases
-// the slot once the unpack has finished, before waiting for the next chunk
-// (a receiver holding slots while it waits could stall a sender that has
-// reserved the next one).
+// Receiver: releases the oldest held slot once its unpack has finished.
+int release_held(pace_kv_channel* ch, bool wait) {
+  const uint32_t idx = (ch->ctl->tail.load(std::memory_order_relaxed)) % ch->ctl->num_slots;
+  hipEvent_t e = ch->dev_unpacked[idx];
+  int rc = PACE_KV_OK;
+  if (wait) {
+    rc = hip_status(hipEventSynchronize(e), "channel unpack out of the device ring");
+  } else {
+    const hipError_t q = hipEventQuery(e);
+    if (q == hipErrorNotReady) return PACE_KV_OK;  // still reading: keep the slot
+    rc = hip_status(q, "channel unpack out of the device ring");
+  }
+  if (rc) return rc;
+  --ch->rx_held;
+  release(ch);
+  return PACE_KV_OK;
+}
+
+// Receiver: gives every held slot back, after the unpacks enqueued on
+// `stream` have stopped reading them; returns rc.
+int release_all_held(pace_kv_channel* ch, int rc, hipStream_t stream) {
+  if (ch->rx_held > 0) (void)hipStreamSynchronize(stream);
+  while (ch->rx_held > 0) {
+    --ch->rx_held;
+    release(ch);
+  }
+  return rc;
+}
+
+// Receiver: a chunk read but not unpacked (its unpack could not be
+// enqueued) also goes back, and the rest of the message is dropped by the
+// next header receive.
+int fail_rx_device(pace_kv_channel* ch, int rc, hipStream_t stream) {
+  release_all_held(ch, rc, stream);
+  (void)hipStreamSynchronize(stream);
+  release(ch);
+  ch->rx_active = false;
+  return rc;
+}
+
+// Receiver: unpacks every chunk straight out of its device slot.  A slot
+// goes back to the sender once its unpack has finished, in ring order.
+// While it waits for the next chunk, the receiver keeps at most
+// num_slots - 2 slots whose unpacks are still in flight, so that its GPU
+// queue does not drain between chunks; the sender, which reserves one slot
+// beyond the chunk it publishes, can then always publish the chunk waited for.
+// With two slots every unpack finishes before the next wait.
 int recv_device(pace_kv_channel* ch, void* const* dst_layers, int64_t pool_pages, const int32_t* page_ids,
                 int32_t* err_count, int timeout_ms, hipStream_t stream) {
   PACE_KV_TRY(ring_ready(ch));
   const Chunking k = ch->rx_chunks;
+  const uint32_t max_held = ch->ctl->num_slots - 2;
   while (ch->rx_active) {
+    // release what has finished, and enough to stay within max_held
+    while (ch->rx_held > 0) {
+      const uint32_t before = ch->rx_held;
+      const int rc = release_held(ch, ch->rx_held > max_held);
+      if (rc) {
+        ch->rx_active = false;
+        return release_all_held(ch, rc, stream);
+      }
+      if (ch->rx_held == before) break;   // the oldest is still in flight
+    }
     uint32_t idx = 0;
     Chunking::Chunk ck;
-    PACE_KV_TRY(next_chunk(ch, timeout_ms, &idx, &ck));
+    // A failed wait (deadline, closed channel, abandoned or unexpected
+    // record) leaves rx_active as next_chunk set it: after a deadline the
+    // message is still pending and can be received or drained again.
+    int rc = next_chunk(ch, timeout_ms, &idx, &ck);
+    if (rc) return release_all_held(ch, rc, stream);
     const int64_t stride = k.layers_per_chunk > 0 ? k.layer_bytes : ck.bytes;
-    int rc = pace_kv_unpack(dev_slot(ch, idx), stride, dst_layers + ck.layer, ck.nl, pool_pages,
-                            page_ids + ck.j0, ck.nj, k.page_bytes, err_count, stream);
+    rc = pace_kv_unpack(dev_slot(ch, idx), stride, dst_layers + ck.layer, ck.nl, pool_pages, page_ids + ck.j0,
+                        ck.nj, k.page_bytes, err_count, stream);
     if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(ch->dev_unpacked[idx], stream), "channel recv record");
-    if (rc == PACE_KV_OK)
-      rc = hip_status(hipEventSynchronize(ch->dev_unpacked[idx]), "channel unpack out of the device ring");
-    if (rc) {
-      // The slot goes back to the sender only after an unpack that was
-      // enqueued has stopped reading it.
-      (void)hipStreamSynchronize(stream);
-      return fail_rx(ch, rc);
-    }
-    finish_chunk(ch);
+    if (rc) return fail_rx_device(ch, rc, stream);
+    ++ch->rx_held;
+    if (++ch->rx_next == k.num_chunks) ch->rx_active = false;
+  }
+  // the message is read: its slots go back as their unpacks finish
+  while (ch->rx_held > 0) {
+    const int rc = release_held(ch, true);
+    if (rc) return release_all_held(ch, rc, stream);
   }
   return PACE_KV_OK;
 }

@@ -408,7 +408,7 @@ def run_pair_device(dev_slot, send, recv, host_slot=4096, num_slots=4):
 # takes, one page, a two-slot ring
 DEVICE_CASES = [(32, 64, (2, 16, 8, 128), 20, 4 << 20, 4), (4, 300, (2, 16, 8, 128), 200, 1 << 20, 4),
                 (70, 16, (2, 16, 1, 64), 9, 1 << 20, 4), (2, 8, (2, 16, 8, 128), 1, 1 << 20, 4),
-                (8, 128, (2, 16, 8, 128), 100, 1 << 20, 2)]
+                (8, 128, (2, 16, 8, 128), 100, 1 << 20, 2), (16, 64, (2, 16, 8, 128), 30, 1 << 20, 8)]
 
 
 @pytest.mark.parametrize("L,pages,shape,n,slot,slots", DEVICE_CASES)
