@@ -40,11 +40,15 @@ def rand_pool(L, pages, shape, dtype, dev, seed):
             for _ in range(L)]
 
 
-def run_pair(slot_bytes, num_slots, send, recv):
-    """Runs send(tx) on a thread and recv(rx) here; returns send's result."""
+def run_pair(slot_bytes, num_slots, send, recv, device_slot_bytes=0):
+    """Runs send(tx) on a thread and recv(rx) here; returns send's result.
+    device_slot_bytes > 0: the channel also has a device ring (same GPU), so
+    device payloads go through it."""
     nm = name()
-    rx = KVChannel.create(nm, slot_bytes, num_slots, 4)
+    rx = KVChannel.create(nm, slot_bytes, num_slots, 4, device_slot_bytes=device_slot_bytes)
     tx = KVChannel.open(nm, 4, timeout=10)
+    if device_slot_bytes:
+        assert tx.device_ring() == (device_slot_bytes, True)
     out, errs = [], []
 
     def sender():
@@ -206,8 +210,13 @@ def make_worker(dev, seed, free_list=None):
     return KVWorker(h, WorkerSequenceManager(P, POOL, free_list=free_list)), cache
 
 
+# the worker-level tests run over the shared-memory ring and over the device ring
+RINGS = {"host": 0, "device": 1 << 20}
+
+
+@pytest.mark.parametrize("ring", RINGS)
 @pytest.mark.parametrize("tokens_src,tokens_dst", [(40, 40), (48, 49)])
-def test_worker_send_and_receive(gpu, tokens_src, tokens_dst):
+def test_worker_send_and_receive(gpu, tokens_src, tokens_dst, ring):
     """prefill side _send_kv_cache (frees the source pages) -> KVref on the
     control plane -> decode side _recv_kv_cache with LIFO allocation and the
     n / n+1 remap; the same destination bytes as _get_kv_cache + KVobj +
@@ -227,7 +236,8 @@ def test_worker_send_and_receive(gpu, tokens_src, tokens_dst):
     def recv(rx):
         got["status"] = dst_w._recv_kv_cache(dst_seq, rx, gpu, timeout=30)
 
-    ref, rank = run_pair(1 << 20, 4, lambda tx: src_w._send_kv_cache(seq, tx, 1.0, 2.0), recv)
+    print(f"worker send/receive over the {ring} ring, {tokens_src} -> {tokens_dst} tokens", flush=True)
+    ref, rank = run_pair(1 << 20, 4, lambda tx: src_w._send_kv_cache(seq, tx, 1.0, 2.0), recv, RINGS[ring])
     assert isinstance(ref, KVref) and ref.kv_indices == src_table and rank == 0
     assert ref.size == L * len(src_table) * 2 * P * H * D * 2 / 1e6
     assert src_w.seq_manager.block_manager.get_num_free_gpu_blocks() == free_before + len(src_table)
@@ -243,7 +253,8 @@ def test_worker_send_and_receive(gpu, tokens_src, tokens_dst):
         assert torch.equal(words(dst_cache[l][untouched]), before[l][untouched])
 
 
-def test_insertion_threads_share_one_channel(gpu):
+@pytest.mark.parametrize("ring", RINGS)
+def test_insertion_threads_share_one_channel(gpu, ring):
     """Four insertion threads take whichever sequence arrives next from one
     channel (_recv_next_kv_cache), as the reference's insertion threads insert
     whichever transfer finishes first; every sequence lands in its own
@@ -291,7 +302,8 @@ def test_insertion_threads_share_one_channel(gpu):
             tx.send_host(torch.empty((0, 0, 2, P, H, D), dtype=torch.float16),
                          KVref(f"stop{i}", [], 0.0).meta(), timeout=30)
 
-    run_pair(1 << 20, 4, send, recv)
+    print(f"four insertion threads over the {ring} ring", flush=True)
+    run_pair(1 << 20, 4, send, recv, RINGS[ring])
     assert not errors, errors
     for s in seqs:
         st = results[s.seq_id]
@@ -302,7 +314,8 @@ def test_insertion_threads_share_one_channel(gpu):
                 f"{s.seq_id} layer {l}"
 
 
-def test_worker_receive_refusals_drain_the_message(gpu):
+@pytest.mark.parametrize("ring", RINGS)
+def test_worker_receive_refusals_drain_the_message(gpu, ring):
     """A destination without room, and a message for another sequence, return
     False and leave the channel ready for the next message."""
     src_w, src_cache = make_worker(gpu, 6)
@@ -323,7 +336,8 @@ def test_worker_receive_refusals_drain_the_message(gpu):
         results.append(dst_w._recv_kv_cache(Sequence.of_length("s2", 32, P), rx, gpu, timeout=30))
         torch.cuda.synchronize()
 
-    run_pair(1 << 20, 2, send, recv)
+    print(f"worker refusals over the {ring} ring", flush=True)
+    run_pair(1 << 20, 2, send, recv, RINGS[ring])
     assert results[0] is False and results[1] is False
     assert isinstance(results[2], KVStatus) and results[2].status
     dst_table = dst_w.seq_manager._get_block_table(Sequence.of_length("s2", 32, P))
@@ -332,7 +346,8 @@ def test_worker_receive_refusals_drain_the_message(gpu):
                            words(src_cache[l][torch.tensor(tables[2], device=gpu)]))
 
 
-def test_helper_zero_fallback_and_repeated_ids(gpu):
+@pytest.mark.parametrize("ring", RINGS)
+def test_helper_zero_fallback_and_repeated_ids(gpu, ring):
     """A sequence without a block table sends one zero page, as get_kv_cache
     returns it; repeated destination ids keep the last page written, as the
     reference's index_put_ does."""
@@ -363,7 +378,8 @@ def test_helper_zero_fallback_and_repeated_ids(gpu):
         oks.append(dst_w.kvhelper.recv_kv_cache(rx, [20, 21, 20], gpu, timeout=30))
         torch.cuda.synchronize()
 
-    run_pair(1 << 20, 2, send, recv)
+    print(f"zero fallback and repeated ids over the {ring} ring", flush=True)
+    run_pair(1 << 20, 2, send, recv, RINGS[ring])
     assert oks == [True, True]
     for l in range(L):
         assert not dst_cache[l][10].any()
