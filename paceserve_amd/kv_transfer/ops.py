@@ -28,12 +28,17 @@ from .. import _native
 IdsLike = Union[torch.Tensor, Sequence[int]]
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_handle(device: torch.device) -> int:
     """The hipStream_t of torch's current stream on `device`, read without
-    building a Stream object (a few microseconds less per call, which counts
-    against launches of 20 us)."""
+    building a Stream object where torch offers that (a few microseconds less
+    per call, which counts against launches of 20 us)."""
     index = device.index if device.index is not None else torch.cuda.current_device()
-    return torch._C._cuda_getCurrentRawStream(index)
+    if _raw_stream is None:
+        return torch.cuda.current_stream(index).cuda_stream
+    return _raw_stream(index)
 
 
 def _addr(a) -> int:
