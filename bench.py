@@ -923,12 +923,38 @@ def run_promote(dev, steps=100, warmup=10):
                      "gbs": round(w.payload_bytes / (statistics.median(lat) * 1e-6) / 1e9, 2), "runs": len(lat)}
         log(f"promote 4096 tok {name}: p50 {out[name]['p50_us']} us ({out[name]['gbs']} GB/s)")
     out["payload_bytes"] = w.payload_bytes
+    out["c_caller"] = run_promote_c(w)
     # the metric's promote latency: allocation + remap + id upload + pack +
     # unpack, through the single library call
     out["p50_us"] = out["buffer_native"]["p50_us"]
     out["p50_mode"] = ("buffer_native (KVMigrator.promote of list block tables -> pace_kv_promote: plan, ids, "
                        "pack, unpack)")
     return out
+
+
+def run_promote_c(w):
+    """The same promotion timed from C (tests/c_abi/pace_kv_promote_latency,
+    built with the library): pace_kv_promote to the completion of an event
+    after it, with no Python in the loop; buffer and fused modes, 100 runs
+    after 10 warm-ups, and a check of the moved bytes.  None when the program
+    is not built."""
+    import subprocess
+
+    from paceserve_amd.build import C_LATENCY_BIN
+
+    if not C_LATENCY_BIN.exists():
+        log(f"{C_LATENCY_BIN} is not built: no C-caller promote latency")
+        return None
+    sh = w.shape
+    cmd = [str(C_LATENCY_BIN), str(sh.num_layers), str(w.src_pool_pages), str(len(w.src_tables[0])),
+           str(sh.page_bytes), "100", "10"]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        raise RuntimeError(f"{' '.join(cmd)} failed ({r.returncode}): {r.stdout} {r.stderr}")
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    log(f"promote 4096 tok from C: buffer p50 {res['buffer']['p50_us']} us, fused p50 {res['fused']['p50_us']} us, "
+        f"verified {res['verified']}")
+    return res
 
 
 def cpu_sample_layers(w) -> int:

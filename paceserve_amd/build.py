@@ -64,29 +64,42 @@ def build_library(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
-C_CHECK_SRC = REPO_DIR / "tests" / "c_abi" / "pace_kv_check.c"
+C_ABI_DIR = REPO_DIR / "tests" / "c_abi"
+C_CHECK_SRC = C_ABI_DIR / "pace_kv_check.c"
 C_CHECK_BIN = C_CHECK_SRC.with_suffix("")
+# promote latency timed from C (no Python in the loop); bench.py runs it
+C_LATENCY_SRC = C_ABI_DIR / "pace_kv_promote_latency.c"
+C_LATENCY_BIN = C_LATENCY_SRC.with_suffix("")
 
 
-def build_c_check(verbose: bool = False) -> Path:
-    """Compiles the plain-C user of the ABI (tests/c_abi/pace_kv_check.c)
-    against the built library; the binary finds the library through its
-    rpath ($ORIGIN-relative) and the HIP runtime under ROCM_PATH."""
+def build_c_program(src: Path, verbose: bool = False) -> Path:
+    """Compiles a plain-C user of the ABI (tests/c_abi/*.c) against the built
+    library; the binary, written next to its source, finds the library
+    through its rpath ($ORIGIN-relative) and the HIP runtime under
+    ROCM_PATH."""
     rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
-    rel = os.path.relpath(PKG_DIR, C_CHECK_BIN.parent)
+    out = src.with_suffix("")
+    rel = os.path.relpath(PKG_DIR, out.parent)
     cmd = [os.environ.get("CC", "gcc"), "-std=c99", "-O2", "-Wall", "-Werror", "-D__HIP_PLATFORM_AMD__",
-           f"-I{rocm / 'include'}", f"-I{INCLUDE_DIR}", str(C_CHECK_SRC), "-o", str(C_CHECK_BIN),
+           f"-I{rocm / 'include'}", f"-I{INCLUDE_DIR}", str(src), "-o", str(out),
            f"-L{PKG_DIR}", "-lpace_kv", f"-L{rocm / 'lib'}", "-lamdhip64",
            f"-Wl,-rpath,$ORIGIN/{rel}", f"-Wl,-rpath,{rocm / 'lib'}"]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError("C ABI check build failed:\n" + proc.stdout + proc.stderr)
-    return C_CHECK_BIN
+        raise RuntimeError(f"{src.name} build failed:\n" + proc.stdout + proc.stderr)
+    return out
+
+
+def build_c_check(verbose: bool = False) -> Path:
+    """Builds the C programs of tests/c_abi; returns the ABI check's path."""
+    build_c_program(C_LATENCY_SRC, verbose)
+    return build_c_program(C_CHECK_SRC, verbose)
 
 
 if __name__ == "__main__":
     path = build_library(verbose="-v" in sys.argv)
     print(path)
     print(build_c_check(verbose="-v" in sys.argv))
+    print(C_LATENCY_BIN)
