@@ -80,6 +80,9 @@ def parse_args():
                     help="skip timing the paged-append producer kernel")
     ap.add_argument("--no-channel", action="store_true",
                     help="skip timing the cross-process channel (4096-token request between two processes)")
+    ap.add_argument("--no-c-caller", action="store_true",
+                    help="skip timing the promote from C (tests/c_abi/pace_kv_promote_latency, a child process); "
+                         "for runs under a tracer, whose trace should hold this process's launches only")
     ap.add_argument("--no-dropin", action="store_true",
                     help="skip timing KVhelper get_kv_cache + insert_kv_cache against the reference's torch "
                          "code for the same calls (4096-token request)")
@@ -856,7 +859,7 @@ def run_config(args, name: str, dev, staging: dict = None) -> dict:
     return out
 
 
-def run_promote(dev, steps=100, warmup=10):
+def run_promote(dev, steps=100, warmup=10, c_caller=True):
     """p50/p90 latency of promoting one 4096-token request."""
     import torch
 
@@ -923,7 +926,7 @@ def run_promote(dev, steps=100, warmup=10):
                      "gbs": round(w.payload_bytes / (statistics.median(lat) * 1e-6) / 1e9, 2), "runs": len(lat)}
         log(f"promote 4096 tok {name}: p50 {out[name]['p50_us']} us ({out[name]['gbs']} GB/s)")
     out["payload_bytes"] = w.payload_bytes
-    out["c_caller"] = run_promote_c(w)
+    out["c_caller"] = run_promote_c(w) if c_caller else None
     # the metric's promote latency: allocation + remap + id upload + pack +
     # unpack, through the single library call
     out["p50_us"] = out["buffer_native"]["p50_us"]
@@ -1218,6 +1221,10 @@ def summarize_promote(trace_csv: str, bench_json: str, command: str) -> str:
             f"({4 * payload / ((pk + up) * 1e-6) / 1e9:.0f} GB/s of pack+unpack bytes); fused promote p50 "
             f"{pr['fused_native']['p50_us']} us, of which {mv:.1f} us is the move kernel. The rest is host "
             f"time (Python, planning, launch) and completion."]
+    if pr.get("c_caller"):
+        c = pr["c_caller"]
+        out += ["", f"The same call from C (tests/c_abi/pace_kv_promote_latency, in the same run): buffer p50 "
+                f"{c['buffer']['p50_us']} us, fused p50 {c['fused']['p50_us']} us."]
     return "\n".join(out) + "\n"
 
 
@@ -1443,7 +1450,7 @@ def main():
         settle = link_settle(dev)
         log(f"host link settled after {settle['waited_s']} s at {settle['d2h_gbs']} GB/s D2H")
         if not args.no_promote:
-            promote = run_promote(dev)
+            promote = run_promote(dev, c_caller=not args.no_c_caller)
             promote["link_probe"] = settle
         for name in staging_names:
             early_staging[name] = run_staging_leg(args, name, dev)
