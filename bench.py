@@ -1247,7 +1247,13 @@ def summarize_copies(copy_csv: str, kernel_csv: str, bench_json: str, command: s
         if "copyBuffer" in r["Kernel_Name"] and e0 - s0 > min_ns:
             spans["D2H"].append((s0, e0, "blit kernel"))
     k = int(st.get("chunks", 0))
-    last = {d: sorted(v)[-k:] for d, v in spans.items()}
+    # The last round trip: its k host-to-device copies are the run's last
+    # ones; its device-to-host copies are the last k that end before them
+    # (later blits, such as the device-to-device copies beside the copy
+    # ceiling, are not chunk copies).
+    h2d = sorted(spans["H2D"])[-k:]
+    t_end = max(e for _, e, _ in h2d) if h2d else 0
+    last = {"H2D": h2d, "D2H": sorted(x for x in spans["D2H"] if x[1] <= t_end)[-k:]}
     t0 = min(v[0][0] for v in last.values() if v)
     t1 = max(v[-1][1] for v in last.values() if v)
 
