@@ -549,3 +549,69 @@ def test_device_ring_with_a_peer_process(gpu, peer):
             d_ids = torch.arange(40 * r, 40 * r + 40, device=gpu)
             for l in range(32):
                 assert torch.equal(words(dst[l][d_ids]), words(src[l][s_ids])), f"request {r} layer {l}"
+
+
+# ------------------------------------------------------- seeded random sweep
+
+def random_channel_case(seed):
+    """A seeded channel configuration: pool shape, pages sent, slot size and
+    count, and the ring (host slots, or a device ring beside 4 KiB host
+    slots)."""
+    rng = np.random.default_rng(5000 + seed)
+    P = int(rng.choice([1, 3, 16]))
+    H = int(rng.choice([1, 2, 8]))
+    D = int(rng.choice([16, 64, 128]))
+    shape = (2, P, H, D)
+    page_bytes = 2 * P * H * D * 2
+    L = int(rng.integers(1, 81))
+    pages = int(rng.integers(1, 301))
+    n = int(rng.integers(1, pages + 1))
+    slots = int(rng.choice([2, 4, 8]))
+    # slot sizes from one page (at most 2000 chunks per message) up to beyond
+    # a whole layer, in 4 KiB steps
+    lo = max(-(-page_bytes // 4096), -(-(L * n * page_bytes) // (2000 * 4096)))
+    hi = max(lo, -(-(2 * n * page_bytes) // 4096))
+    slot = 4096 * int(rng.integers(lo, hi + 1))
+    slot = min(slot, (1 << 30) // slots)
+    ring = "device" if seed % 2 else "host"
+    return L, pages, shape, n, slot, slots, ring, rng
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_channel_messages(gpu, seed):
+    L, pages, shape, n, slot, slots, ring, rng = random_channel_case(seed)
+    print(f"random channel case {seed}: L={L} pages={pages} shape={shape} n={n} slot={slot} x {slots} "
+          f"ring={ring}", flush=True)
+    src = rand_pool(L, pages, shape, torch.float16, gpu, 30 + seed)
+    dst = rand_pool(L, pages, shape, torch.float16, gpu, 60 + seed)
+    before = [words(d).clone() for d in dst]
+    # three messages of n pages each into disjoint destination pages where
+    # the pool has room for them, else into the same ones (the last wins)
+    msgs = []
+    for m in range(3):
+        s_ids = rng.permutation(pages)[:n].tolist()
+        d_ids = rng.permutation(pages)[:n].tolist()
+        msgs.append((s_ids, d_ids))
+
+    def send(tx):
+        return [tx.send(src, s, f"m{i}".encode(), timeout=30) for i, (s, _) in enumerate(msgs)]
+
+    def recv(rx):
+        for i, (_, d) in enumerate(msgs):
+            h = rx.recv_header(timeout=30)
+            assert (h.meta, h.num_layers, h.n_pages) == (f"m{i}".encode(), L, n)
+            rx.recv(dst, d, timeout=30)
+        torch.cuda.synchronize()
+
+    if ring == "device":
+        run_pair_device(slot, send, recv, num_slots=slots)
+    else:
+        run_pair(slot, slots, send, recv)
+    # the expected destination: torch's scatter of torch's gather, message by message
+    want = [b.clone() for b in before]
+    for s_ids, d_ids in msgs:
+        si, di = torch.tensor(s_ids, device=gpu), torch.tensor(d_ids, device=gpu)
+        for l in range(L):
+            want[l][di] = words(src[l])[si]
+    for l in range(L):
+        assert torch.equal(words(dst[l]), want[l]), f"layer {l}"
