@@ -59,7 +59,7 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default=workloads.DEFAULT, choices=workloads.NAMES)
+    ap.add_argument("--workload", default=workloads.DEFAULT, choices=workloads.NAMES + workloads.SHARDS)
     ap.add_argument("--mode", default="buffer", choices=["buffer", "fused"],
                     help="buffer: pack + unpack (the metric); fused: pool-to-pool move")
     ap.add_argument("--no-cpu", action="store_true")
@@ -1506,7 +1506,7 @@ def main():
     configs = None
     if not args.no_configs:
         configs = {name: run_config(args, name, dev, early_staging.get(name))
-                   for name in workloads.NAMES if name != w.name}
+                   for name in workloads.NAMES + workloads.SHARDS if name != w.name}
     if staging is None and early_staging:
         staging = next(iter(early_staging.values()))
 

@@ -29,6 +29,11 @@ benchmark and the tests build identical source block tables and pages:
   llama3-8b-4096tok-bf16     Llama-3-8B KV, bf16: one 4096-token request (256
                              pages) in a 2048-page pool (the promote-latency
                              workload).  Seed 1100.
+  llama3-70b-256req-bf16-tp8 one GPU's share of llama3-70b-256req-bf16 under
+                             tensor parallelism 8: the same requests and block
+                             tables, with the 8 KV heads split one per GPU, so
+                             each page is 8 KiB (2 x 16 x 1 x 128 x 2 B);
+                             moved in 40-layer chunks.  Seed 1005.
 """
 from __future__ import annotations
 
@@ -148,6 +153,9 @@ NAMES = ("llama3-8b-512tok-fp16", "llama3-8b-16req-bf16", "llama2-7b-8x4095tok-f
          "llama3-8b-32768tok-bf16", "llama3-70b-256req-bf16")
 DEFAULT = "llama3-70b-256req-bf16"
 PROMOTE = "llama3-8b-4096tok-bf16"
+# One GPU's share of a sharded migration, at its real shape (each GPU of a
+# tensor-parallel group moves its own head slice of the same pages).
+SHARDS = ("llama3-70b-256req-bf16-tp8",)
 
 
 def get(name: str) -> Workload:
@@ -190,10 +198,12 @@ def get(name: str) -> Workload:
         return Workload(name, "1 x 32768-token request, Llama-3-8B KV, bf16, values U[-4,4], "
                         "2048-page pool in permuted order, on-device and pinned-host",
                         shape, 2048, 2048, lengths, tables, seed, init="uniform4", staging="both")
-    if name == "llama3-70b-256req-bf16":
+    if name in ("llama3-70b-256req-bf16", "llama3-70b-256req-bf16-tp8"):
+        tp8 = name.endswith("-tp8")
         seed = 1005
         rng = np.random.default_rng(seed)
-        shape = KVShape(num_layers=80, num_kv_heads=8, head_dim=128, page_size=16, dtype=torch.bfloat16)
+        shape = KVShape(num_layers=80, num_kv_heads=1 if tp8 else 8, head_dim=128, page_size=16,
+                        dtype=torch.bfloat16)
         lengths = rng.integers(64, 2049, size=256).tolist()
         need = [_pages(n, 16) for n in lengths]
         perm = rng.permutation(20480).tolist()
@@ -204,6 +214,11 @@ def get(name: str) -> Workload:
                 if len(tables[r]) < need[r]:
                     tables[r].append(perm[k])
                     k += 1
+        if tp8:
+            return Workload(name, "one GPU's share at tensor parallelism 8 of 256 requests U{64..2048} tokens, "
+                            "Llama-3-70B KV (80 layers, 1 of 8 KV heads: 8 KiB pages), bf16, 20480-page pools "
+                            "dealt round-robin (heavily fragmented), 40-layer chunks",
+                            shape, 20480, 20480, lengths, tables, seed, device_layers_per_chunk=40)
         return Workload(name, "256 requests U{64..2048} tokens, Llama-3-70B KV (80 layers), bf16, "
                         "20480-page pools dealt round-robin (heavily fragmented), 8-layer chunks",
                         shape, 20480, 20480, lengths, tables, seed, device_layers_per_chunk=8)
@@ -215,7 +230,7 @@ def get(name: str) -> Workload:
         tables = [rng.permutation(2048)[:256].tolist()]
         return Workload(name, "1 x 4096-token request, Llama-3-8B KV, bf16, 2048-page pools",
                         shape, 2048, 2048, lengths, tables, seed)
-    raise ValueError(f"unknown workload {name!r} (known: {', '.join(NAMES + (PROMOTE,))})")
+    raise ValueError(f"unknown workload {name!r} (known: {', '.join(NAMES + SHARDS + (PROMOTE,))})")
 
 
 def _fill_layer(t: torch.Tensor, g: torch.Generator, init: str) -> None:

@@ -1,4 +1,5 @@
-"""The five reference-shaped workloads at full size on the GPU.
+"""The five reference-shaped workloads at full size on the GPU, and one GPU's
+share of the 70B workload under tensor parallelism 8 (8 KiB pages).
 
 For each: plan (LIFO destination allocation + remap), move the pages through
 the HIP path, then check every layer of both pools exactly, as raw bytes
@@ -65,7 +66,7 @@ def run_buffer(w, src, dst, plan, dev):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("c", workloads.NAMES)
+@pytest.mark.parametrize("c", workloads.NAMES + workloads.SHARDS)
 def test_workload_buffer_path(gpu, c):
     w, src, dst, plan, s_ids, d_ids = setup(c, gpu)
     print(f"{w.name}: {plan.n_pages} pages x {w.shape.num_layers} layers", flush=True)
