@@ -1426,7 +1426,7 @@ def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build runs on one GPU: the KV migration path is measured on "
+        print(json.dumps({"error": "this benchmark runs on one GPU: the KV migration path is measured on "
                           "one device's share; --gpus N>1 is not supported"}), flush=True)
         sys.exit(2)
 
