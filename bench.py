@@ -15,16 +15,19 @@ the stream the kernels run on, over the K timed steps.  Inputs are resident in
 HBM before timing starts.  After the timed steps every layer of both pools is
 compared byte for byte with torch's own gather/scatter of the same pages
 (`verified`).  Also reported: the roofline of the copy kernel (algorithmic
-bytes per launch / mean launch time vs 8 TB/s), the other four workloads in the
-same process (`configs`: GB/s, fraction of peak and the same exact check; the
+bytes per launch / mean launch time vs 8 TB/s), the other four workloads and
+one GPU's share of the 70B workload at tensor parallelism 8 in the same
+process (`configs`: GB/s, fraction of peak and the same exact check; the
 pinned-host legs of the two that have one, `staging`), p50/p90 promote latency
 of one 4096-token request (dst allocation + remap + block-table H2D + pack +
-unpack, to completion) and the reference's CPU path (torch index_select /
-index_copy_ on host tensors) timed on a bounded sample on this host's cores.
+unpack, to completion; also timed from C) and the reference's CPU path (torch
+index_select / index_copy_ on host tensors) timed on a bounded sample on this
+host's cores.
 
 Usage: python bench.py [--steps K] [--warmup W] [--workload NAME]
-       [--no-cpu] [--no-promote] [--no-verify] [--no-configs]
-(NAME: one of paceserve_amd.workloads.NAMES; see that module)
+       [--no-cpu] [--no-promote] [--no-verify] [--no-configs] ...
+(NAME: one of paceserve_amd.workloads.NAMES or SHARDS; see that module and
+--help for the other legs' switches)
 """
 from __future__ import annotations
 
