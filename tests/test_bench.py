@@ -150,3 +150,18 @@ def test_summarize_kernel_pmc_groups_by_kernel_and_grid(tmp_path):
     assert "| append_kernel<2, false, false, true> | 32768 | 1 | 7 | 14 |" in md
     assert "| append_kernel<2, false, false, true> | 2097152 | 2 | 200 | 400 |" in md
     assert "other" not in md
+
+
+def test_tp8_share_is_the_70b_workload_with_one_kv_head():
+    """One GPU's share at tensor parallelism 8 moves the same requests and
+    block tables as the 70B workload, with 8 KiB pages (1 of 8 KV heads), so
+    its payload is exactly an eighth."""
+    from paceserve_amd import workloads
+
+    full, share = workloads.get("llama3-70b-256req-bf16"), workloads.get("llama3-70b-256req-bf16-tp8")
+    assert share.name in workloads.SHARDS and share.name not in workloads.NAMES
+    assert share.src_tables == full.src_tables and share.lengths == full.lengths
+    assert (share.src_pool_pages, share.dst_pool_pages) == (full.src_pool_pages, full.dst_pool_pages)
+    assert share.shape.num_kv_heads * 8 == full.shape.num_kv_heads and share.shape.page_bytes == 8192
+    assert share.payload_bytes * 8 == full.payload_bytes
+    assert share.device_layers_per_chunk <= 64        # one launch per chunk
