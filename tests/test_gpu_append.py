@@ -189,3 +189,54 @@ def test_append_of_70000_tokens(gpu):
     # the 5 tokens request 1 held before the append are untouched
     first = kv_indices.long()[npages[0]]
     assert torch.equal(words(cache[first, :, :5]), words(before[first, :, :5]))
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_appends_match_numpy(gpu, seed):
+    """Seeded random batches through both forms: 1-1000 requests (the fused
+    form's request search takes more than one round of 256 past 256
+    requests), prior lengths 0-99, 0-40 new tokens per request, random row
+    shapes and element types.  Expected: every appended row placed by numpy at
+    kv_indices[kv_indptr[b] + pos // P], slot pos % P, pos counted from the end
+    of the request's tokens; every other slot unchanged."""
+    rng = np.random.default_rng(7000 + seed)
+    R = int(rng.choice([1, 7, 64, 257, 600, 1000]))
+    P = int(rng.choice([1, 4, 16]))
+    H, D = int(rng.choice([1, 2, 8])), int(rng.choice([16, 64, 128]))
+    dtype = [torch.float16, torch.bfloat16, torch.float32, torch.float8_e4m3fn][int(rng.integers(0, 4))]
+    esz = torch.empty(0, dtype=dtype).element_size()
+    prior = rng.integers(0, 100, R)
+    app = rng.integers(0, 41, R)
+    total = prior + app
+    pages = -(-total // P)
+    NP = int(pages.sum()) + 3
+    kv_indptr = np.concatenate([[0], np.cumsum(pages)])
+    kv_indices = rng.permutation(NP)[: kv_indptr[-1]]
+    last = np.where(total == 0, 0, np.where(total % P == 0, P, total % P))
+    append_indptr = np.concatenate([[0], np.cumsum(app)])
+    nnz = int(append_indptr[-1])
+    print(f"random append seed {seed}: R={R} P={P} H={H} D={D} {dtype} nnz={nnz} pages={NP}", flush=True)
+    raw = lambda shape: torch.from_numpy(rng.integers(-2 ** 7, 2 ** 7, shape).astype(np.int8)).to(gpu)
+    k = raw((nnz, H, D * esz)).view(dtype).view(nnz, H, D)
+    v = raw((nnz, H, D * esz)).view(dtype).view(nnz, H, D)
+    cache = raw((NP, 2, P, H, D * esz)).view(dtype).view(NP, 2, P, H, D)
+    # numpy placement of every appended token
+    want = words(cache).cpu().numpy().copy()
+    kw, vw = words(k).cpu().numpy(), words(v).cpu().numpy()
+    b = np.repeat(np.arange(R), app)
+    pos = total[b] - app[b] + (np.arange(nnz) - append_indptr[b])
+    page = kv_indices[kv_indptr[b] + pos // P]
+    want[page, 0, pos % P] = kw
+    want[page, 1, pos % P] = vw
+    two = cache.clone()
+    seq = ap.get_seq_lens(i32(kv_indptr, gpu), i32(last, gpu), P)
+    bi, ps = ap.get_batch_indices_positions(i32(append_indptr, gpu), seq, nnz)
+    ap.append_paged_kv_cache(k, v, bi, ps, two, i32(kv_indices, gpu), i32(kv_indptr, gpu), i32(last, gpu))
+    fused = cache.clone()
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ap.append_paged_kv_cache_indptr(k, v, i32(append_indptr, gpu), fused, i32(kv_indices, gpu),
+                                    i32(kv_indptr, gpu), i32(last, gpu), err=err)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(words(two).cpu().numpy(), want)
+    np.testing.assert_array_equal(words(fused).cpu().numpy(), want)
+    assert int(err.item()) == 0
