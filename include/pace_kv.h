@@ -211,6 +211,13 @@ int pace_kv_unpack_from_host(pace_kv_stager* stager, const void* host_in,
  * does not overlap the previous chunk's copy).  Chunks are whole layers when
  * one layer's n_pages * page_bytes fits the scratch, else runs of pages of
  * one layer; a page larger than the scratch is rejected (PACE_KV_ERANGE).
+ * host_out must be pinned host memory (hipHostMalloc) whose allocation
+ * holds the whole payload from host_out on; pageable memory is rejected
+ * (PACE_KV_EINVAL), since the runtime would stage its copies through buffers
+ * of its own, and a payload past the allocation's end is rejected
+ * (PACE_KV_ERANGE).  The check sees allocations, not the caller's view of
+ * them: a buffer carved out of a larger pinned allocation is the caller's
+ * to size.
  * It calls no hipMalloc or hipFree.  Every call on one GPU shares that GPU's
  * scratch: calls on one stream from one host thread are ordered, while calls
  * that overlap (on several streams, or from several host threads) race on it.

@@ -61,6 +61,34 @@ int current_scratch(char** out) {
   return PACE_KV_OK;
 }
 
+// host_out of the allocation-free pack: pinned host memory (hipHostMalloc or
+// torch's pin_memory) holding `bytes` from host_out on.  With pageable memory
+// the runtime would stage each copy through buffers of its own, and the copy
+// could not run under graph capture.
+int check_pinned_host_out(const void* host_out, int64_t bytes) {
+  hipPointerAttribute_t attr;
+  memset(&attr, 0, sizeof(attr));
+  hipError_t e = hipPointerGetAttributes(&attr, host_out);
+  if (e != hipSuccess || attr.type != hipMemoryTypeHost) {
+    (void)hipGetLastError();
+    return fail(PACE_KV_EINVAL, "pack_to_host_noalloc: host_out is not pinned host memory (hipHostMalloc)");
+  }
+  hipDeviceptr_t start = nullptr;
+  size_t size = 0;
+  e = hipMemGetAddressRange(&start, &size, const_cast<void*>(host_out));
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(PACE_KV_EINVAL, "pack_to_host_noalloc: the range of host_out's allocation is unknown");
+  }
+  const uintptr_t begin = reinterpret_cast<uintptr_t>(host_out);
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(start);
+  if (begin < lo || begin - lo + static_cast<uint64_t>(bytes) > size)
+    return fail(PACE_KV_ERANGE, "pack_to_host_noalloc: host_out's allocation holds %zu bytes from its start, "
+                "the payload needs %lld from offset %llu", size, (long long)bytes,
+                (unsigned long long)(begin - lo));
+  return PACE_KV_OK;
+}
+
 }  // namespace
 
 struct pace_kv_stager {
@@ -356,6 +384,8 @@ int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers, 
   if (n_pages > INT64_MAX / page_bytes) return fail(PACE_KV_ERANGE, "payload size overflows");
   if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
   if (host_out == nullptr) return fail(PACE_KV_EINVAL, "pack_to_host_noalloc: host_out is NULL");
+  if (num_layers > INT64_MAX / (n_pages * page_bytes)) return fail(PACE_KV_ERANGE, "payload size overflows");
+  PACE_KV_TRY(check_pinned_host_out(host_out, num_layers * n_pages * page_bytes));
   char* slot = nullptr;
   PACE_KV_TRY(current_scratch(&slot));
   hipStream_t stream = static_cast<hipStream_t>(stream_);

@@ -60,3 +60,24 @@ def test_noalloc_matches_pack_to_host_on_two_calls(gpu):
         assert torch.equal(got, want), f"{n} pages: noalloc differs from pack_to_host"
         gathered = torch.stack([t.index_select(0, ids.long()) for t in pool.layers]).cpu()
         assert torch.equal(got, gathered.view(torch.uint8).reshape(-1)), f"{n} pages: differs from torch gather"
+
+
+def test_noalloc_refuses_pageable_host_memory(gpu):
+    """host_out must be pinned: pageable memory is refused before any copy and
+    stays untouched, and a valid call right after works."""
+    pool = ops.PagedPool(workloads.fill_pool(64, SHAPE, 32, "normal", gpu))
+    ids = torch.tensor([3, 7, 1], dtype=torch.int32, device=gpu)
+    need = pool.num_layers * 3 * pool.page_bytes
+    lib = _native.load()
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    pageable = torch.full((need,), SENTINEL, dtype=torch.uint8)
+    rc = lib.pace_kv_pack_to_host_noalloc(pool.table(), pool.num_layers, pool.num_pages, ids.data_ptr(), 3,
+                                          pool.page_bytes, pageable.data_ptr(), None, stream)
+    torch.cuda.synchronize()
+    assert rc == _native.PACE_KV_EINVAL and b"not pinned" in lib.pace_kv_last_error()
+    assert bool((pageable == SENTINEL).all())
+    good = host_buffer(pool, 3)
+    noalloc(pool, ids, good)
+    torch.cuda.synchronize()
+    gathered = torch.stack([t.index_select(0, ids.long()) for t in pool.layers]).cpu()
+    assert torch.equal(good, gathered.view(torch.uint8).reshape(-1))
