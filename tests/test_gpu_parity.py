@@ -307,3 +307,56 @@ def test_concurrent_host_threads_on_their_own_streams(gpu):
         di = torch.tensor(d_ids, device=gpu)
         for l in range(L):
             assert same(dst[l].index_select(0, di), src[l].index_select(0, si))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_staging_matches_torch(gpu, seed):
+    """Seeded random pinned-host legs through one stager: layer counts on both
+    sides of the 64-layer launch split, pages of 64 B to 64 KiB (whole and
+    partial 1 KiB rows), four element types, 1 to all layers per chunk, 2-5
+    slots, and a host ring of one chunk up to the whole payload; pack to host,
+    unpack from host and the round trip, each compared with torch's gather
+    and scatter, twice in a row on the same stager with different batches."""
+    rng = np.random.default_rng(9000 + seed)
+    L = int(rng.choice([1, 3, 8, 33, 70]))
+    shape = (2, int(rng.choice([1, 4, 16])), int(rng.choice([1, 2, 8])), int(rng.choice([8, 64, 128])))
+    dtype = [torch.float16, torch.bfloat16, torch.float32, torch.uint8][int(rng.integers(0, 4))]
+    esz = torch.empty(0, dtype=dtype).element_size()
+    page_bytes = int(np.prod(shape)) * esz
+    pages = int(rng.integers(1, 200))
+    k = int(rng.integers(1, L + 1))                   # layers per chunk
+    slots = int(rng.integers(2, 6))
+    src = rand_pool(L, pages, shape, dtype, gpu, 100 + seed)
+    dst = rand_pool(L, pages, shape, dtype, gpu, 200 + seed)
+    chunk = -(-(k * pages * page_bytes) // 256) * 256  # slots hold k layers of up to all pages
+    print(f"random staging seed {seed}: L={L} shape={shape} {dtype} pages={pages} k={k} slots={slots}",
+          flush=True)
+    with ops.Stager(chunk, slots) as st:
+        for rep in range(2):
+            n = int(rng.integers(1, pages + 1))
+            s_ids = rng.permutation(pages)[:n].tolist()
+            d_ids = rng.permutation(pages)[:n].tolist()
+            si, di = torch.tensor(s_ids, device=gpu), torch.tensor(d_ids, device=gpu)
+            ref = torch.stack([words(s)[si] for s in src])                     # [L, n, ...] on the device
+            expect = [words(d).clone() for d in dst]
+            for l in range(L):
+                expect[l][di] = ref[l]
+            # pack to host
+            host = torch.empty((L, n) + shape, dtype=dtype, pin_memory=True)
+            st.pack_to_host(src, s_ids, host, k)
+            torch.cuda.current_stream().synchronize()
+            assert torch.equal(words(host), ref.cpu()), f"rep {rep}: pack_to_host"
+            # unpack from host
+            got = [d.clone() for d in dst]
+            st.unpack_from_host(host, got, d_ids, k)
+            torch.cuda.current_stream().synchronize()
+            for l in range(L):
+                assert torch.equal(words(got[l]), expect[l]), f"rep {rep}: unpack_from_host layer {l}"
+            # round trip through a host ring of one chunk up to the whole payload
+            ring_chunks = int(rng.integers(1, -(-L // k) + 1))
+            ring = torch.empty(ring_chunks * k * n * page_bytes, dtype=torch.uint8, pin_memory=True)
+            got = [d.clone() for d in dst]
+            st.roundtrip(src, s_ids, got, d_ids, ring, k)
+            torch.cuda.current_stream().synchronize()
+            for l in range(L):
+                assert torch.equal(words(got[l]), expect[l]), f"rep {rep}: roundtrip layer {l}"
