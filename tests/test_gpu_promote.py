@@ -176,3 +176,53 @@ def test_native_promote_normalises_negative_ids_and_rejects_out_of_range(gpu):
         with pytest.raises(IndexError, match="out of bounds for dimension 0 with size 2048"):
             a.promote([bad], mode="buffer")
         assert a.dst_allocator.free_blocks == free_before
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_promotions_match_torch(gpu, seed):
+    """Seeded random batches promoted back to back through one migrator on the
+    native allocator: 1-6 requests of 1-200 pages (inline ids up to 512
+    pages, uploaded ids above), n or n+1 destination pages per request, the
+    buffer, fused or pinned mode, 1 to all layers per chunk.  Each promotion
+    must pop the destination tables a Python LIFO allocator with the same
+    free list pops, and leave the destination pool equal to torch's scatter
+    of torch's gather into the pages those tables name (every other page
+    unchanged); the source pool stays unchanged."""
+    rng = np.random.default_rng(8000 + seed)
+    src, dst = pools(gpu, 40 + seed)
+    free = rng.permutation(POOL).tolist()
+    alloc = NativeBlockAllocator(16, POOL, free)
+    mirror = BlockAllocator(16, POOL, free)               # the expected LIFO order
+    mig = migrate.KVMigrator(src, dst, alloc)
+    host = torch.empty(SHAPE.num_layers * POOL * src.page_bytes, dtype=torch.uint8, pin_memory=True)
+    src_before = [words(t).clone() for t in src.layers]
+    for call in range(3):
+        R = int(rng.integers(1, 7))
+        sizes = rng.integers(1, 201, R)
+        if call == 2:                           # a batch above 512 pages: ids uploaded, not inline
+            R, sizes = 6, rng.integers(100, 201, 6)
+        tables = [rng.permutation(POOL)[: int(k)].tolist() for k in sizes]
+        dst_pages = [len(t) + int(rng.integers(0, 2)) for t in tables]
+        mode = ["buffer", "fused", "pinned"][int(rng.integers(0, 3))]
+        if call == 2:
+            mode = ["buffer", "fused"][seed % 2]
+        k = int(rng.integers(1, SHAPE.num_layers + 1))
+        print(f"random promote seed {seed} call {call}: {R} requests, {sum(sizes)} pages, {mode}, "
+              f"{k} layers per chunk", flush=True)
+        expect_plan = migrate.plan_batch(tables, POOL, mirror, dst_pages)
+        dst_before = [words(t).clone() for t in dst.layers]
+        plan = mig.promote(tables, dst_pages, mode=mode, layers_per_chunk=k,
+                           host_buf=host if mode == "pinned" else None)
+        torch.cuda.synchronize()
+        assert plan.dst_tables == expect_plan.dst_tables and plan.dst_ids == expect_plan.dst_ids
+        si = torch.tensor(expect_plan.src_ids, dtype=torch.long, device=gpu)
+        di = torch.tensor(expect_plan.dst_ids, dtype=torch.long, device=gpu)
+        for l in range(SHAPE.num_layers):
+            want = dst_before[l].index_copy_(0, di, words(src.layers[l]).index_select(0, si))
+            assert torch.equal(words(dst.layers[l]), want), f"call {call} layer {l}"
+            assert torch.equal(words(src.layers[l]), src_before[l]), f"call {call} source layer {l}"
+        # the requests finish: their pages go back to both allocators alike
+        done = [p for t in plan.dst_tables for p in t]
+        alloc.free_many(reversed(done))
+        mirror.free_many(reversed(done))
+    assert alloc.free_blocks == mirror.free_blocks
