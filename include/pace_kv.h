@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define PACE_KV_ABI_VERSION 1
+#define PACE_KV_ABI_VERSION 2
 
 /* Largest number of layers one kernel launch addresses; entry points split
  * longer layer lists into several launches on the same stream. */
@@ -211,22 +211,25 @@ int pace_kv_unpack_from_host(pace_kv_stager* stager, const void* host_in,
  * does not overlap the previous chunk's copy).  Chunks are whole layers when
  * one layer's n_pages * page_bytes fits the scratch, else runs of pages of
  * one layer; a page larger than the scratch is rejected (PACE_KV_ERANGE).
- * host_out must be pinned host memory (hipHostMalloc) whose allocation
- * holds the whole payload from host_out on; pageable memory is rejected
- * (PACE_KV_EINVAL), since the runtime would stage its copies through buffers
- * of its own, and a payload past the allocation's end is rejected
- * (PACE_KV_ERANGE).  The check sees allocations, not the caller's view of
- * them: a buffer carved out of a larger pinned allocation is the caller's
- * to size.
- * It calls no hipMalloc or hipFree.  Every call on one GPU shares that GPU's
+ * host_out must be pinned host memory (hipHostMalloc) and host_out_bytes the
+ * bytes the caller gives it: a payload (num_layers * n_pages * page_bytes)
+ * larger than host_out_bytes, or running past the end of host_out's pinned
+ * allocation, is rejected (PACE_KV_ERANGE) before anything is enqueued.
+ * Pageable memory is rejected (PACE_KV_EINVAL), since the runtime would stage
+ * its copies through buffers of its own.
+ * It calls no hipMalloc or hipFree, and once a call has run on a device (the
+ * first call looks up that device's scratch address) later calls there make
+ * only kernel launches and hipMemcpyAsync copies on `stream`, so they can be
+ * captured into a HIP graph.  Every call on one GPU shares that GPU's
  * scratch: calls on one stream from one host thread are ordered, while calls
- * that overlap (on several streams, or from several host threads) race on it.
+ * that overlap (on several streams, or from several host threads, or a graph
+ * replayed beside other calls) race on it.
  */
 int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers,
                                  int64_t pool_pages, const int32_t* page_ids,
                                  int64_t n_pages, int64_t page_bytes,
-                                 void* host_out, int32_t* err_count,
-                                 void* stream);
+                                 void* host_out, int64_t host_out_bytes,
+                                 int32_t* err_count, void* stream);
 
 /*
  * Full host round trip in one pipeline: pack(c) -> D2H(c) -> H2D(c) ->
@@ -420,9 +423,13 @@ int pace_kv_promote(pace_kv_promoter* promoter, pace_kv_allocator* dst_alloc,
  * sends (whole messages) and its own receives.  Every blocking call waits at
  * most timeout_ms milliseconds (PACE_KV_ETIMEDOUT; 0 = do not wait) and
  * returns PACE_KV_ECLOSED once either side has closed the channel or the peer
- * process has exited (checked at least every 10 ms while waiting).  A sender
- * that fails after the header marks the message abandoned, and the
- * receiver's next wait for its chunks fails with PACE_KV_ESTATE.
+ * process has exited (checked at least every 10 ms while waiting).  A send
+ * on a closed channel fails with PACE_KV_ECLOSED before it writes anything;
+ * a receiver still takes the messages published before the sender closed
+ * (those in shared-memory slots, and those in device slots while the ring is
+ * alive: see pace_kv_channel_create_device).  A sender that fails after the
+ * header marks the message abandoned, and the receiver's next wait for its
+ * chunks fails with PACE_KV_ESTATE.
  *
  * Replaces the transfer of a KVobj from a prefill instance to a decode
  * instance through Ray's object store (paceserve/disutil/prefill_instance.py:
@@ -446,9 +453,16 @@ int pace_kv_channel_create(const char* name, int64_t slot_bytes, int num_slots,
  * packs each chunk straight into a device slot (chunks sized to
  * dev_slot_bytes), and the receiving endpoint unpacks straight out of it, so
  * the payload never leaves HBM; the other endpoint opens the ring on its
- * first device transfer.  Sends from another GPU, and send_host, use the
- * shared-memory slots as before.  Replaces, for two instance processes on one
- * GPU, the same object-store hop as pace_kv_channel_create
+ * first device transfer.  Sends from another GPU, sends while the receiver's
+ * GPU (recorded at its last pace_kv_channel_recv_header) is another one or
+ * none, and send_host, use the shared-memory slots as before.
+ * Lifetime: endpoints in the creator's process share the ring, which is
+ * freed when the last of them closes, in any order.  Another process that
+ * has opened the ring uses it only while the creator's endpoint is open:
+ * once the creator has closed, its sends and its receives of device-slot
+ * messages fail with PACE_KV_ECLOSED, so the creator must outlive the
+ * device transfers of its peers.  Replaces, for two instance processes on
+ * one GPU, the same object-store hop as pace_kv_channel_create
  * (paceserve/disutil/prefill_instance.py:96-107,
  *  paceserve/disutil/decode_instance.py:165-171). */
 int pace_kv_channel_create_device(const char* name, int64_t slot_bytes,

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (binds the HIP runtime before the library loads)
 
 LIB_PATH = Path(__file__).resolve().parent / "libpace_kv.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 MAX_LAYERS_PER_LAUNCH = 64
 NOALLOC_SCRATCH_BYTES = 64 << 20
 
@@ -82,7 +82,8 @@ SIGNATURES = {
     "pace_kv_channel_recv": (
         c_int, [_VP, _VP, c_int, c_int64, _VP, c_int64, c_int64, _VP, c_int, _VP]),
     "pace_kv_channel_recv_host": (c_int, [_VP, _VP, c_int64, c_int]),
-    "pace_kv_pack_to_host_noalloc": (c_int, [_VP, c_int, c_int64, _VP, c_int64, c_int64, _VP, _VP, _VP]),
+    "pace_kv_pack_to_host_noalloc": (
+        c_int, [_VP, c_int, c_int64, _VP, c_int64, c_int64, _VP, c_int64, _VP, _VP]),
     "pace_kv_roundtrip": (
         c_int,
         [_VP, _VP, c_int64, _VP, _VP, c_int64, _VP, c_int, c_int64, c_int64, c_int, _VP, c_int64,

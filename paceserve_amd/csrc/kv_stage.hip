@@ -373,7 +373,8 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
 
 int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers, int64_t pool_pages,
                                  const int32_t* page_ids, int64_t n_pages, int64_t page_bytes,
-                                 void* host_out, int32_t* err_count, void* stream_) {
+                                 void* host_out, int64_t host_out_bytes, int32_t* err_count,
+                                 void* stream_) {
   const int64_t cap = PACE_KV_NOALLOC_SCRATCH_BYTES;
   if (num_layers < 0 || n_pages < 0) return fail(PACE_KV_EINVAL, "negative num_layers or n_pages");
   if (page_bytes <= 0 || page_bytes % 16 != 0)
@@ -385,7 +386,11 @@ int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers, 
   if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
   if (host_out == nullptr) return fail(PACE_KV_EINVAL, "pack_to_host_noalloc: host_out is NULL");
   if (num_layers > INT64_MAX / (n_pages * page_bytes)) return fail(PACE_KV_ERANGE, "payload size overflows");
-  PACE_KV_TRY(check_pinned_host_out(host_out, num_layers * n_pages * page_bytes));
+  const int64_t payload = num_layers * n_pages * page_bytes;
+  if (payload > host_out_bytes)
+    return fail(PACE_KV_ERANGE, "pack_to_host_noalloc: the payload needs %lld bytes, host_out holds %lld",
+                (long long)payload, (long long)host_out_bytes);
+  PACE_KV_TRY(check_pinned_host_out(host_out, payload));
   char* slot = nullptr;
   PACE_KV_TRY(current_scratch(&slot));
   hipStream_t stream = static_cast<hipStream_t>(stream_);

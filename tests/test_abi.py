@@ -112,11 +112,20 @@ def test_noalloc_pack_to_host_rejects_pages_beyond_its_scratch(lib):
     """A page larger than the 64 MiB scratch is refused before any device
     call (so this runs without a GPU), with the limit in the message."""
     big = _native.NOALLOC_SCRATCH_BYTES + 16
-    rc = lib.pace_kv_pack_to_host_noalloc(_layers(1), 1, 4, 0x100, 1, big, 0x1000, None, None)
+    rc = lib.pace_kv_pack_to_host_noalloc(_layers(1), 1, 4, 0x100, 1, big, 0x1000, 1 << 40, None, None)
     assert rc == _native.PACE_KV_ERANGE
     assert b"exceeds the 67108864-byte scratch" in lib.pace_kv_last_error()
-    assert lib.pace_kv_pack_to_host_noalloc(_layers(1), 1, 4, 0x100, 1, 24, 0x1000, None, None) == \
+    assert lib.pace_kv_pack_to_host_noalloc(_layers(1), 1, 4, 0x100, 1, 24, 0x1000, 1 << 40, None, None) == \
         _native.PACE_KV_EINVAL                                      # not a multiple of 16
-    assert lib.pace_kv_pack_to_host_noalloc(None, 0, 4, None, 3, 65536, None, None, None) == 0   # no work
+    assert lib.pace_kv_pack_to_host_noalloc(None, 0, 4, None, 3, 65536, None, 0, None, None) == 0   # no work
+
+
+def test_noalloc_pack_to_host_rejects_a_short_output(lib):
+    """A payload larger than host_out_bytes is refused before any device call
+    (so this runs without a GPU): 3 layers x 2 pages x 4 KiB need 24 KiB, one
+    byte more than the caller gives."""
+    rc = lib.pace_kv_pack_to_host_noalloc(_layers(3), 3, 4, 0x100, 2, 4096, 0x1000, 3 * 2 * 4096 - 1, None, None)
+    assert rc == _native.PACE_KV_ERANGE
+    assert b"needs 24576 bytes, host_out holds 24575" in lib.pace_kv_last_error()
     text = HEADER.read_text()
     assert "#define PACE_KV_NOALLOC_SCRATCH_BYTES (64 << 20)" in text

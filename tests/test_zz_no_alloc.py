@@ -3,7 +3,10 @@ called through the C ABI and compared with pace_kv_pack_to_host (a stager's
 pipeline) and with torch's gather: the same host bytes on two calls in a row,
 the first with layers larger than the scratch (runs of pages), the second
 smaller (several layers per chunk), so that the second call's output cannot
-pass on bytes left in the scratch by the first."""
+pass on bytes left in the scratch by the first; a host_out one byte short
+is refused before anything is written; and the call captured into a HIP
+graph, replayed over changed pool contents, writes torch's gather each time
+and allocates no device memory."""
 import numpy as np
 import pytest
 import torch
@@ -18,12 +21,13 @@ POOL = 2048
 SENTINEL = 0xA5
 
 
-def noalloc(pool, ids, host):
+def noalloc(pool, ids, host, host_bytes=None):
     lib = _native.load()
     stream = torch.cuda.current_stream(pool.device).cuda_stream
+    nbytes = host.numel() * host.element_size() if host_bytes is None else host_bytes
     _native.check(lib.pace_kv_pack_to_host_noalloc(
         pool.table(), pool.num_layers, pool.num_pages, ids.data_ptr(), ids.numel(), pool.page_bytes,
-        host.data_ptr(), None, stream))
+        host.data_ptr(), nbytes, None, stream))
 
 
 def staged(pool, ids, host):
@@ -72,7 +76,7 @@ def test_noalloc_refuses_pageable_host_memory(gpu):
     stream = torch.cuda.current_stream(gpu).cuda_stream
     pageable = torch.full((need,), SENTINEL, dtype=torch.uint8)
     rc = lib.pace_kv_pack_to_host_noalloc(pool.table(), pool.num_layers, pool.num_pages, ids.data_ptr(), 3,
-                                          pool.page_bytes, pageable.data_ptr(), None, stream)
+                                          pool.page_bytes, pageable.data_ptr(), need, None, stream)
     torch.cuda.synchronize()
     assert rc == _native.PACE_KV_EINVAL and b"not pinned" in lib.pace_kv_last_error()
     assert bool((pageable == SENTINEL).all())
@@ -81,3 +85,71 @@ def test_noalloc_refuses_pageable_host_memory(gpu):
     torch.cuda.synchronize()
     gathered = torch.stack([t.index_select(0, ids.long()) for t in pool.layers]).cpu()
     assert torch.equal(good, gathered.view(torch.uint8).reshape(-1))
+
+
+def gather(pool, ids):
+    return torch.stack([t.index_select(0, ids.long()) for t in pool.layers]).cpu().view(torch.uint8).reshape(-1)
+
+
+def test_noalloc_refuses_a_short_output(gpu):
+    """A host_out one byte shorter than the payload is refused with
+    PACE_KV_ERANGE before anything is enqueued, although the pinned
+    allocation behind it is large enough (a short view of a larger block);
+    the buffer stays untouched and the same call with the full size works."""
+    pool = ops.PagedPool(workloads.fill_pool(64, SHAPE, 36, "normal", gpu))
+    ids = torch.tensor([5, 60, 2, 33], dtype=torch.int32, device=gpu)
+    need = pool.num_layers * 4 * pool.page_bytes
+    host = torch.full((need + 4096,), SENTINEL, dtype=torch.uint8, pin_memory=True)
+    lib = _native.load()
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    rc = lib.pace_kv_pack_to_host_noalloc(pool.table(), pool.num_layers, pool.num_pages, ids.data_ptr(), 4,
+                                          pool.page_bytes, host.data_ptr(), need - 1, None, stream)
+    torch.cuda.synchronize()
+    assert rc == _native.PACE_KV_ERANGE, lib.pace_kv_last_error()
+    assert f"needs {need} bytes, host_out holds {need - 1}".encode() in lib.pace_kv_last_error()
+    assert bool((host == SENTINEL).all())
+    noalloc(pool, ids, host, need)
+    torch.cuda.synchronize()
+    assert torch.equal(host[:need], gather(pool, ids))
+    assert bool((host[need:] == SENTINEL).all())
+
+
+def test_noalloc_replays_from_a_hip_graph(gpu):
+    """One call captured with torch.cuda.graph after a warm-up call outside
+    capture (which looks up the scratch address), then replayed three times
+    over pool contents rewritten in place between the replays (two different
+    seeds, then the first again), with eager work and synchronisations in
+    between: every replay's host bytes equal torch's gather of the contents
+    at that time.  Repeated calls, eager and replayed, leave the device's
+    free memory unchanged."""
+    pool_pages, n = 512, 200
+    pool = ops.PagedPool(workloads.fill_pool(pool_pages, SHAPE, 37, "normal", gpu))
+    rng = np.random.default_rng(37)
+    ids = torch.tensor(rng.permutation(pool_pages)[:n], dtype=torch.int32, device=gpu)
+    host = host_buffer(pool, n)
+    noalloc(pool, ids, host)                       # warm-up, outside capture
+    torch.cuda.synchronize()
+    assert torch.equal(host, gather(pool, ids))
+    graph = torch.cuda.CUDAGraph()
+    print("noalloc: capturing one call", flush=True)
+    with torch.cuda.graph(graph):
+        noalloc(pool, ids, host)
+    torch.cuda.synchronize()
+    for seed in (38, 39, 38):
+        fresh = workloads.fill_pool(pool_pages, SHAPE, seed, "normal", gpu)
+        for dst, src in zip(pool.layers, fresh):
+            dst.copy_(src)
+        del fresh
+        host.fill_(SENTINEL)
+        torch.cuda.synchronize()
+        print(f"noalloc: replay over seed {seed}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(host, gather(pool, ids)), f"replay over seed {seed}"
+    free_before = torch.cuda.mem_get_info(gpu)[0]
+    for _ in range(3):
+        noalloc(pool, ids, host)
+        graph.replay()
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info(gpu)[0] == free_before
+    assert torch.equal(host, gather(pool, ids))
