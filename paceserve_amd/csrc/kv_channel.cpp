@@ -67,7 +67,7 @@ using pace_kv::hip_status;
 namespace {
 
 constexpr uint64_t kMagic = 0x50414345'4b564348ull;  // "PACEKVCH"
-constexpr uint32_t kVersion = 3;
+constexpr uint32_t kVersion = 4;
 constexpr int kMaxSlots = 64;
 constexpr int kNameMax = 200;
 // Largest device ring: one shared allocation, kept well under the 2 GiB
@@ -126,6 +126,14 @@ struct alignas(64) ChannelCtl {
   int32_t dev_pad;
   char dev_bus_id[kBusIdBytes];
   hipIpcMemHandle_t dev_handle;
+  // The creator has closed its endpoint: a ring it exported is freed (or
+  // about to be), so other processes no longer touch it.
+  std::atomic<uint32_t> creator_closed;
+  // PCI bus id of the GPU that was current when the receiver last asked for
+  // a header, as 8 words of 8 bytes (all zero: not known yet; kNoGpu: the
+  // receiver had no GPU).  A sender uses the device ring only when the
+  // receiver is not known yet or is on the ring's GPU.
+  std::atomic<uint64_t> rx_bus_id[kBusIdBytes / 8];
 };
 
 // head and tail count records modulo 2^32 and a record's slot is the count
@@ -397,8 +405,8 @@ struct pace_kv_channel {
   // this process's view of the device ring
   char* dev_ring = nullptr;
   int dev_device = -1;
-  bool dev_allocated = false;  // hipMalloc'ed here (freed at close)
-  bool dev_imported = false;   // opened from the exported handle (closed at close)
+  bool dev_local = false;     // allocated by this process: holds a reference in g_rings
+  bool dev_imported = false;  // opened from the exported handle (closed at close)
   std::vector<hipEvent_t> dev_packed;    // sender: pack into slot i finished
   std::vector<hipEvent_t> dev_unpacked;  // receiver: unpack out of slot i finished
 };
@@ -413,15 +421,19 @@ char* slot_data(pace_kv_channel* ch, uint32_t idx) {
 // when it may have made cond() true; closing the channel also wakes it.  The
 // peer process is checked at every wake-up (at least every 10 ms), so a wait
 // on a peer that died ends then rather than at the deadline.
+// A sender's wait (closed_first) fails on a closed channel even when cond()
+// holds, so nothing is published into a channel either side has closed; a
+// receiver's wait still takes records published before the sender closed.
 template <class Cond>
 int wait_for(pace_kv_channel* ch, std::atomic<uint32_t>* word, const ProcessId& peer, Cond cond,
-             int timeout_ms, const char* what) {
+             int timeout_ms, const char* what, bool closed_first = false) {
   using clock = std::chrono::steady_clock;
   const auto deadline = clock::now() + std::chrono::milliseconds(timeout_ms < 0 ? 0 : timeout_ms);
   for (int spin = 0;; ++spin) {
     const uint32_t seen = word->load(std::memory_order_acquire);
-    if (cond()) return PACE_KV_OK;
-    if (ch->ctl->closed.load(std::memory_order_acquire))
+    const bool closed = ch->ctl->closed.load(std::memory_order_acquire) != 0;
+    if (!(closed && closed_first) && cond()) return PACE_KV_OK;
+    if (closed)
       return fail(PACE_KV_ECLOSED, "channel %s: closed while waiting for %s", ch->name.c_str(), what);
     if (spin < 256) {
       __builtin_ia32_pause();
@@ -446,7 +458,7 @@ int acquire_slot(pace_kv_channel* ch, int timeout_ms, uint32_t* idx) {
   const uint32_t h = c->head.load(std::memory_order_relaxed);
   PACE_KV_TRY(wait_for(ch, &c->tail, c->receiver,
                        [&] { return h - c->tail.load(std::memory_order_acquire) < c->num_slots; },
-                       timeout_ms, "a free slot"));
+                       timeout_ms, "a free slot", true));
   *idx = h % c->num_slots;
   return PACE_KV_OK;
 }
@@ -517,9 +529,17 @@ void free_staging(Staging& s) {
 // Process-local registry of the device rings this process allocated, by the
 // inode of their channel's shared-memory object: an endpoint that opens a
 // channel created in its own process uses the ring's address directly, since
-// an exported handle is not opened in the process that exported it.
+// an exported handle is not opened in the process that exported it.  Each
+// endpoint of this process holds one reference to the ring while it is open
+// (the creator from its creation, another endpoint from its open), and the
+// ring is freed when the last of them closes, whichever closes first.
+struct RingRef {
+  char* ring = nullptr;
+  int device = -1;  // the device it was allocated on
+  int refs = 0;
+};
 std::mutex g_rings_mu;
-std::map<uint64_t, char*> g_rings;
+std::map<uint64_t, RingRef> g_rings;
 
 uint64_t shm_inode(int fd) {
   struct stat st;
@@ -536,16 +556,21 @@ void free_device_ring(pace_kv_channel* ch) {
   }
   if (ch->dev_ring != nullptr) {
     if (ch->dev_imported) (void)hipIpcCloseMemHandle(ch->dev_ring);
-    if (ch->dev_allocated) {
+    if (ch->dev_local) {
+      char* last = nullptr;
       {
         std::lock_guard<std::mutex> lock(g_rings_mu);
-        g_rings.erase(shm_inode(ch->fd));
+        auto it = g_rings.find(shm_inode(ch->fd));
+        if (it != g_rings.end() && it->second.ring == ch->dev_ring && --it->second.refs == 0) {
+          last = it->second.ring;
+          g_rings.erase(it);
+        }
       }
-      (void)hipFree(ch->dev_ring);
+      if (last != nullptr) (void)hipFree(last);
     }
   }
   ch->dev_ring = nullptr;
-  ch->dev_imported = ch->dev_allocated = false;
+  ch->dev_imported = ch->dev_local = false;
 }
 
 void destroy(pace_kv_channel* ch) {
@@ -662,6 +687,13 @@ int abandon(pace_kv_channel* ch, uint64_t id, int rc) {
   return rc;
 }
 
+// Sender: nothing goes into a channel that either side has closed.
+int check_open(pace_kv_channel* ch) {
+  if (ch->ctl->closed.load(std::memory_order_acquire))
+    return fail(PACE_KV_ECLOSED, "channel %s is closed", ch->name.c_str());
+  return PACE_KV_OK;
+}
+
 int check_rx_shape(pace_kv_channel* ch, int num_layers, int64_t n_pages, int64_t page_bytes) {
   if (!ch->rx_active)
     return fail(PACE_KV_ESTATE, "channel %s: no message header received", ch->name.c_str());
@@ -714,6 +746,41 @@ int device_ring_here(pace_kv_channel* ch, bool* here) {
   return PACE_KV_OK;
 }
 
+constexpr uint64_t kNoGpu = ~uint64_t(0);
+
+// Receiver: records the GPU current in this thread (or that there is none)
+// for the sender's choice of ring.
+void record_receiver_gpu(pace_kv_channel* ch) {
+  uint64_t words[kBusIdBytes / 8] = {0};
+  int dev = -1;
+  char bus[kBusIdBytes] = {0};
+  if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetPCIBusId(bus, kBusIdBytes, dev) == hipSuccess) {
+    bus[kBusIdBytes - 1] = '\0';
+    memcpy(words, bus, sizeof(words));
+  } else {
+    (void)hipGetLastError();
+    words[0] = kNoGpu;
+  }
+  for (int i = 0; i < kBusIdBytes / 8; ++i) ch->ctl->rx_bus_id[i].store(words[i], std::memory_order_relaxed);
+}
+
+// Sender: whether the receiver can take a message in device slots: its GPU
+// is not known yet, or it is the ring's GPU.
+bool receiver_on_ring_gpu(pace_kv_channel* ch) {
+  uint64_t words[kBusIdBytes / 8];
+  bool unknown = true;
+  for (int i = 0; i < kBusIdBytes / 8; ++i) {
+    words[i] = ch->ctl->rx_bus_id[i].load(std::memory_order_relaxed);
+    unknown = unknown && words[i] == 0;
+  }
+  if (unknown) return true;
+  if (words[0] == kNoGpu) return false;
+  char bus[kBusIdBytes];
+  memcpy(bus, words, sizeof(bus));
+  bus[kBusIdBytes - 1] = '\0';
+  return strncmp(bus, ch->ctl->dev_bus_id, kBusIdBytes) == 0;
+}
+
 int make_slot_events(pace_kv_channel* ch) {
   const size_t n = ch->ctl->num_slots;
   for (std::vector<hipEvent_t>* v : {&ch->dev_packed, &ch->dev_unpacked}) {
@@ -736,6 +803,9 @@ int ring_ready(pace_kv_channel* ch) {
   if (strncmp(bus, c->dev_bus_id, kBusIdBytes) != 0)
     return fail(PACE_KV_ESTATE, "channel %s: its device ring is on the GPU at %.64s, the current GPU is at %s",
                 ch->name.c_str(), c->dev_bus_id, bus);
+  if (ch->dev_imported && c->creator_closed.load(std::memory_order_acquire))
+    return fail(PACE_KV_ECLOSED, "channel %s: the process that created its device ring has closed it",
+                ch->name.c_str());
   if (ch->dev_ring != nullptr) {
     if (dev != ch->dev_device)
       return fail(PACE_KV_ESTATE, "channel %s: device ring mapped on device %d, device %d is current",
@@ -749,8 +819,13 @@ int ring_ready(pace_kv_channel* ch) {
     if (it == g_rings.end())
       return fail(PACE_KV_ESTATE, "channel %s: its device ring was allocated by this process and is freed",
                   ch->name.c_str());
-    p = it->second;
+    p = it->second.ring;
+    ++it->second.refs;
+    ch->dev_local = true;
   } else {
+    if (c->creator_closed.load(std::memory_order_acquire))
+      return fail(PACE_KV_ECLOSED, "channel %s: the process that created its device ring has closed it",
+                  ch->name.c_str());
     PACE_KV_TRY(hip_status(hipIpcOpenMemHandle(&p, c->dev_handle, hipIpcMemLazyEnablePeerAccess),
                            "hipIpcOpenMemHandle (channel device ring)"));
     ch->dev_imported = true;
@@ -770,7 +845,7 @@ int acquire_slot_at(pace_kv_channel* ch, uint32_t pos, int timeout_ms, uint32_t*
   ChannelCtl* c = ch->ctl;
   PACE_KV_TRY(wait_for(ch, &c->tail, c->receiver,
                        [&] { return pos - c->tail.load(std::memory_order_acquire) < c->num_slots; },
-                       timeout_ms, "a free slot"));
+                       timeout_ms, "a free slot", true));
   *idx = pos % c->num_slots;
   return PACE_KV_OK;
 }
@@ -923,13 +998,20 @@ int recv_device(pace_kv_channel* ch, void* const* dst_layers, int64_t pool_pages
   return PACE_KV_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-}  // extern "C"
-
-namespace {
+// An endpoint opened in the process that created the channel's device ring
+// shares that ring from the start (one more reference), so that the ring
+// outlives the creator's endpoint while this one is open.
+void take_local_ring(pace_kv_channel* ch) {
+  ChannelCtl* c = ch->ctl;
+  if (c->dev_slot_bytes <= 0 || c->dev_owner_pid != static_cast<int32_t>(getpid())) return;
+  std::lock_guard<std::mutex> lock(g_rings_mu);
+  auto it = g_rings.find(shm_inode(ch->fd));
+  if (it == g_rings.end()) return;
+  ++it->second.refs;
+  ch->dev_ring = it->second.ring;
+  ch->dev_device = it->second.device;
+  ch->dev_local = true;
+}
 
 // Creates the ring (and, with dev_slot_bytes > 0, the device ring on the
 // current GPU); the magic goes in last.
@@ -1000,6 +1082,8 @@ int create_channel(const char* name, int64_t slot_bytes, int num_slots, int copy
   }
   c->dev_slot_bytes = 0;
   c->dev_owner_pid = 0;
+  c->creator_closed.store(0);
+  for (auto& w : c->rx_bus_id) w.store(0);
   if (dev_slot_bytes > 0) {
     int dev = -1;
     void* ring = nullptr;
@@ -1009,9 +1093,9 @@ int create_channel(const char* name, int64_t slot_bytes, int num_slots, int copy
     if (rc == PACE_KV_OK) {
       ch->dev_ring = static_cast<char*>(ring);
       ch->dev_device = dev;
-      ch->dev_allocated = true;
+      ch->dev_local = true;
       std::lock_guard<std::mutex> lock(g_rings_mu);
-      g_rings[shm_inode(ch->fd)] = ch->dev_ring;
+      g_rings[shm_inode(ch->fd)] = RingRef{ch->dev_ring, dev, 1};
     }
     if (rc == PACE_KV_OK)
       rc = hip_status(hipIpcGetMemHandle(&c->dev_handle, ring), "hipIpcGetMemHandle (channel device ring)");
@@ -1094,6 +1178,7 @@ int pace_kv_channel_open(const char* name, int copy_threads, int timeout_ms, pac
     return fail(PACE_KV_ESTATE, "channel %s: incompatible control block", name);
   }
   ch->pool = new CopyPool(copy_threads);
+  take_local_ring(ch);
   *out = ch;
   return PACE_KV_OK;
 }
@@ -1101,6 +1186,7 @@ int pace_kv_channel_open(const char* name, int copy_threads, int timeout_ms, pac
 int pace_kv_channel_close(pace_kv_channel* ch) {
   if (ch == nullptr) return PACE_KV_OK;
   if (ch->ctl) {
+    if (ch->creator) ch->ctl->creator_closed.store(1, std::memory_order_release);
     ch->ctl->closed.store(1, std::memory_order_release);
     wake_all(&ch->ctl->head);
     wake_all(&ch->ctl->tail);
@@ -1135,11 +1221,13 @@ int pace_kv_channel_send(pace_kv_channel* ch, const void* const* src_layers, int
                          void* stream_) {
   if (ch == nullptr) return fail(PACE_KV_EINVAL, "channel is NULL");
   std::lock_guard<std::mutex> lock(ch->send_mu);
+  PACE_KV_TRY(check_open(ch));
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   bool device = false;
   if (num_layers > 0 && n_pages > 0) {
     if (src_layers == nullptr || page_ids == nullptr) return fail(PACE_KV_EINVAL, "channel send: NULL argument");
     PACE_KV_TRY(device_ring_here(ch, &device));
+    device = device && receiver_on_ring_gpu(ch);
   }
   if (device) {
     // Same GPU as the device ring: the payload never leaves HBM.
@@ -1194,6 +1282,7 @@ int pace_kv_channel_send_host(pace_kv_channel* ch, const void* payload, int num_
                               uint64_t* msg_id) {
   if (ch == nullptr) return fail(PACE_KV_EINVAL, "channel is NULL");
   std::lock_guard<std::mutex> lock(ch->send_mu);
+  PACE_KV_TRY(check_open(ch));
   Chunking k;
   PACE_KV_TRY(make_chunking(num_layers, n_pages, page_bytes, ch->ctl->slot_bytes, &k));
   if (k.num_chunks > 0 && payload == nullptr) return fail(PACE_KV_EINVAL, "channel send: payload is NULL");
@@ -1216,6 +1305,7 @@ int pace_kv_channel_recv_header(pace_kv_channel* ch, void* meta, int64_t meta_ca
   if (ch->rx_active)
     return fail(PACE_KV_ESTATE, "channel %s: the payload of message %llu has not been received",
                 ch->name.c_str(), (unsigned long long)ch->rx_msg);
+  if (ch->ctl->dev_slot_bytes > 0) record_receiver_gpu(ch);
   uint32_t idx = 0;
   for (;;) {
     PACE_KV_TRY(next_record(ch, timeout_ms, &idx, "a message"));

@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 import torch
 
+from paceserve_amd import workloads
 from paceserve_amd.core.sequence import Sequence
 from paceserve_amd.kv_transfer.channel import KVChannel, KVref
 from paceserve_amd.kv_transfer.kv_utils import KVhelper
@@ -38,6 +39,21 @@ def rand_pool(L, pages, shape, dtype, dev, seed):
     g = torch.Generator(device=dev).manual_seed(seed)
     return [torch.randn((pages,) + shape, generator=g, device=dev, dtype=torch.float32).to(dtype)
             for _ in range(L)]
+
+
+# The three requests the cross-process tests send: request r moves source
+# pages r, r+3, ... (40 of them) into destination pages 40r .. 40r+39.
+PEER_SRC_IDS = [p for r in range(3) for p in list(range(r, 128, 3))[:40]]
+PEER_DST_IDS = list(range(120))
+
+
+def peer_mismatch(src, dst, dev):
+    """Whole-layer check of the three requests into a zeroed destination
+    (workloads.migration_mismatch: every page of every layer, so a stray
+    write into a page no request names fails)."""
+    return workloads.migration_mismatch(src, dst, torch.tensor(PEER_SRC_IDS, device=dev),
+                                        torch.tensor(PEER_DST_IDS, device=dev),
+                                        (torch.zeros_like(s) for s in src))
 
 
 def run_pair(slot_bytes, num_slots, send, recv, device_slot_bytes=0):
@@ -165,11 +181,7 @@ def test_sender_in_another_process(gpu):
         if child.poll() is None:
             child.kill()
         rx.close()
-    for r in range(3):
-        s_ids = torch.tensor(list(range(r, 128, 3))[:40], device=gpu)
-        d_ids = torch.arange(40 * r, 40 * r + 40, device=gpu)
-        for l in range(32):
-            assert torch.equal(words(dst[l][d_ids]), words(src[l][s_ids])), f"request {r} layer {l}"
+    assert peer_mismatch(src, dst, gpu) is None
 
 
 # ---------------------------------------------------------- worker methods
@@ -261,6 +273,8 @@ def test_insertion_threads_share_one_channel(gpu, ring):
     destination pages."""
     src_w, src_cache = make_worker(gpu, 10)
     dst_w, dst_cache = make_worker(gpu, 11)
+    before = [c.clone() for c in dst_cache]
+    src_before = [c.clone() for c in src_cache]
     lengths = [16 * k for k in (3, 1, 4, 2, 5, 2, 3, 1)]
     seqs = [Sequence.of_length(f"s{i}", n, P) for i, n in enumerate(lengths)]
     for s in seqs:
@@ -312,6 +326,13 @@ def test_insertion_threads_share_one_channel(gpu, ring):
         for l in range(L):
             assert torch.equal(words(dst_cache[l][torch.tensor(table, device=gpu)]), words(want[s.seq_id][l])), \
                 f"{s.seq_id} layer {l}"
+    # every page of every layer of both caches: each sequence's pages where its
+    # table points, the pages no sequence received untouched, the source unchanged
+    s_ids = torch.tensor([p for s in seqs for p in src_tables[s.seq_id]], device=gpu)
+    d_ids = torch.tensor([p for s in seqs for p in dst_w.seq_manager._get_block_table(dst_seqs[s.seq_id])],
+                         device=gpu)
+    bad = workloads.migration_mismatch(src_cache, dst_cache, s_ids, d_ids, before, src_before)
+    assert bad is None, bad
 
 
 @pytest.mark.parametrize("ring", RINGS)
@@ -484,9 +505,54 @@ def test_device_ring_to_host_discard_and_host_messages(gpu):
     assert torch.equal(words(back), words(want))
 
 
+@pytest.mark.parametrize("creator", ["sender", "receiver"])
+def test_device_ring_outlives_its_creator_in_one_process(gpu, creator):
+    """Two endpoints of one process share the device ring, which is freed
+    when the last of them closes.  The creator closes first: as the sender,
+    the message it published is still received out of the ring; as the
+    receiver, a later send into the closed channel fails with
+    PACE_KV_ECLOSED before it packs anything."""
+    from paceserve_amd import _native
+
+    print(f"device ring, creator = {creator}, creator closes first", flush=True)
+    L, pages, shape = 3, 16, (2, 16, 8, 128)
+    src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 40)
+    dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 41)
+    before = [d.clone() for d in dst]
+    s_ids, d_ids = [3, 9, 0, 15, 7], [12, 1, 4, 8, 2]
+    nm = name()
+    first = KVChannel.create(nm, 4096, 4, 2, device_slot_bytes=1 << 20)
+    second = KVChannel.open(nm, 2, timeout=10)
+    tx, rx = (first, second) if creator == "sender" else (second, first)
+    try:
+        # 3 layers x 5 pages x 64 KiB: one chunk in one 1 MiB device slot, so
+        # the send returns once the message is in the ring
+        tx.send(src, s_ids, b"m", timeout=30)
+        if creator == "sender":
+            first.close()
+        h = rx.recv_header(timeout=30)
+        assert (h.meta, h.num_layers, h.n_pages) == (b"m", L, 5)
+        assert rx.device_ring() == (1 << 20, True)
+        rx.recv(dst, d_ids, timeout=30)
+        torch.cuda.synchronize()
+        if creator == "receiver":
+            first.close()
+            with pytest.raises(_native.PaceKVError) as e:
+                tx.send(src, [1, 2], b"late", timeout=30)
+            assert e.value.status == _native.PACE_KV_ECLOSED
+            torch.cuda.synchronize()
+    finally:
+        for ch in (first, second):
+            ch.close()
+    bad = workloads.migration_mismatch(src, dst, torch.tensor(s_ids, device=gpu), torch.tensor(d_ids, device=gpu),
+                                       before)
+    assert bad is None, bad
+
+
 DEVICE_PEER = r"""
 import sys, torch
 sys.path.insert(0, {root!r})
+from paceserve_amd import workloads
 from paceserve_amd.kv_transfer.channel import KVChannel
 dev = torch.device("cuda", 0)
 g = torch.Generator(device=dev).manual_seed(78)
@@ -505,11 +571,10 @@ else:
         assert h.meta == ("request %d" % r).encode() and h.n_pages == 40, h
         ch.recv(dst, list(range(40 * r, 40 * r + 40)), timeout=60)
     torch.cuda.synchronize()
-    for r in range(3):
-        s_ids = torch.tensor(list(range(r, 128, 3))[:40], device=dev)
-        d_ids = torch.arange(40 * r, 40 * r + 40, device=dev)
-        for l in range(32):
-            assert torch.equal(dst[l][d_ids].view(torch.int16), src[l][s_ids].view(torch.int16)), (r, l)
+    # every page of every layer: the three requests' pages, zeros elsewhere
+    bad = workloads.migration_mismatch(src, dst, torch.tensor({src_ids}, device=dev),
+                                       torch.tensor({dst_ids}, device=dev), (torch.zeros_like(s) for s in src))
+    assert bad is None, bad
 print("peer done", flush=True)
 ch.close()
 """
@@ -524,7 +589,8 @@ def test_device_ring_with_a_peer_process(gpu, peer):
     dev_slot = 4 << 20                                  # 40 pages x 64 KiB: whole layers, 4 MiB slots
     ch = KVChannel.create(nm, 4096, 4, 2, device_slot_bytes=dev_slot)
     child = subprocess.Popen([sys.executable, "-c",
-                              DEVICE_PEER.format(root=str(ROOT), name=nm, dev_slot=dev_slot, role=peer)])
+                              DEVICE_PEER.format(root=str(ROOT), name=nm, dev_slot=dev_slot, role=peer,
+                                                 src_ids=PEER_SRC_IDS, dst_ids=PEER_DST_IDS)])
     try:
         g = torch.Generator(device=gpu).manual_seed(78)
         src = [torch.randn((128, 2, 16, 8, 128), generator=g, device=gpu, dtype=torch.float32).to(torch.bfloat16)
@@ -544,11 +610,7 @@ def test_device_ring_with_a_peer_process(gpu, peer):
             child.kill()
         ch.close()
     if peer == "send":
-        for r in range(3):
-            s_ids = torch.tensor(list(range(r, 128, 3))[:40], device=gpu)
-            d_ids = torch.arange(40 * r, 40 * r + 40, device=gpu)
-            for l in range(32):
-                assert torch.equal(words(dst[l][d_ids]), words(src[l][s_ids])), f"request {r} layer {l}"
+        assert peer_mismatch(src, dst, gpu) is None
 
 
 # ------------------------------------------------------- seeded random sweep
