@@ -188,6 +188,8 @@ int promote_inline(pace_kv_promoter* pr, pace_kv_allocator* dst_alloc,
     }
   }
   if (rc) {
+    // As in pace_kv_promote: pages go back once the copies into them are done.
+    (void)hipStreamSynchronize(stream);
     std::lock_guard<std::mutex> lock(dst_alloc->mu);
     unpop_pages(dst_alloc, plan.n_dst_table, out_dst_tables);
   }
@@ -392,9 +394,13 @@ int pace_kv_promote(pace_kv_promoter* pr, pace_kv_allocator* dst_alloc,
   }
   // Record even on failure: the slot's next user waits on this event.
   const int rc2 = hip_status(hipEventRecord(pr->done[s], stream), "promoter record");
-  // On failure the destination pages go back to the free list (any partial
-  // writes into them are ordered before later use on this stream).
-  if (rc) return rollback(rc);
+  if (rc) {
+    // The destination pages go back to the free list only after every copy
+    // enqueued into them has finished, so that their next owner, on any
+    // stream, cannot see a late partial write.
+    (void)hipStreamSynchronize(stream);
+    return rollback(rc);
+  }
   return rc2;
 }
 

@@ -8,8 +8,10 @@
  * the call to the completion of an event recorded after it on the same
  * stream (CLOCK_MONOTONIC); the destination pages go back to the allocator
  * after each run, in the order that makes the next run allocate the same
- * pages.  After the runs, three layers of every moved page (and of the
- * transfer buffer) are checked on the host against the source contents.
+ * pages.  After each mode's runs, three layers of every moved page (and, in
+ * buffer mode, of the transfer buffer) are checked on the host against the
+ * source contents; the destination pool and the buffer are zeroed between
+ * the modes, so a mode that wrote nothing cannot pass on the other's bytes.
  *
  * Usage: pace_kv_promote_latency [layers pool_pages n_pages page_bytes runs warmup]
  * Prints one JSON line: p50/p90 microseconds per mode and whether the check
@@ -131,8 +133,14 @@ int main(int argc, char** argv) {
 
   const char* modes[2] = {"buffer", "fused"};
   double p50[2], p90[2];
+  int ok = 1;
+  const int check_layers[3] = {0, layers / 2, layers - 1};
   for (int m = 0; m < 2; ++m) {
     void* b = m == 0 ? buf : NULL;
+    for (int l = 0; l < layers; ++l)
+      HIP_OK(hipMemsetD32Async((hipDeviceptr_t)dst_layers[l], 0, (size_t)(pool * page_bytes / 4), stream));
+    HIP_OK(hipMemsetD32Async((hipDeviceptr_t)buf, 0, (size_t)(layers * n * page_bytes / 4), stream));
+    HIP_OK(hipStreamSynchronize(stream));
     for (int r = 0; r < warmup + runs; ++r) {
       const double t0 = now_us();
       PACE_OK(pace_kv_promote(pr, alloc, (const void* const*)src_layers, pool, dst_layers, pool, layers,
@@ -148,18 +156,17 @@ int main(int argc, char** argv) {
     qsort(lat + warmup, (size_t)runs, sizeof(double), cmp_double);
     p50[m] = runs % 2 ? lat[warmup + runs / 2] : 0.5 * (lat[warmup + runs / 2 - 1] + lat[warmup + runs / 2]);
     p90[m] = lat[warmup + (int)(0.9 * (runs - 1))];
-  }
-
-  /* the last run's pages: tables[j] of the destination holds src_ids[j] */
-  int ok = 1;
-  const int check_layers[3] = {0, layers / 2, layers - 1};
-  for (int c = 0; c < 3 && ok; ++c) {
-    const int l = check_layers[c];
-    for (int64_t j = 0; j < n && ok; ++j) {
-      const uint32_t want = word_of(l, src_ids[j]);
-      ok = page_is((char*)dst_layers[l] + tables[j] * page_bytes, page_bytes, want, scratch) &&
-           page_is((char*)buf + (l * n + j) * page_bytes, page_bytes, want, scratch);
+    /* the last run's pages: tables[j] of the destination holds src_ids[j]
+     * (and so does page j of the buffer in buffer mode) */
+    for (int c = 0; c < 3 && ok; ++c) {
+      const int l = check_layers[c];
+      for (int64_t j = 0; j < n && ok; ++j) {
+        const uint32_t want = word_of(l, src_ids[j]);
+        ok = page_is((char*)dst_layers[l] + tables[j] * page_bytes, page_bytes, want, scratch) &&
+             (b == NULL || page_is((char*)buf + (l * n + j) * page_bytes, page_bytes, want, scratch));
+      }
     }
+    if (!ok) fprintf(stderr, "%s mode: a moved page differs from its source\n", modes[m]);
   }
 
   printf("{\"layers\": %d, \"pool_pages\": %lld, \"n_pages\": %lld, \"page_bytes\": %lld, \"runs\": %d, "
