@@ -18,7 +18,8 @@ compared byte for byte with torch's own gather/scatter of the same pages
 bytes per launch / mean launch time vs 8 TB/s), the other four workloads and
 one GPU's share of the 70B workload at tensor parallelism 8 in the same
 process (`configs`: GB/s, fraction of peak and the same exact check; the
-pinned-host legs of the two that have one, `staging`), p50/p90 promote latency
+pinned-host legs of the two that have one, `staging`, run first in the
+process and again at its end, `staging_warm`), p50/p90 promote latency
 of one 4096-token request (dst allocation + remap + block-table H2D + pack +
 unpack, to completion; also timed from C) and the reference's CPU path (torch
 index_select / index_copy_ on host tensors) timed on a bounded sample on this
@@ -77,6 +78,8 @@ def parse_args():
                     help="after timing, run torch's contiguous copy of 1 GiB three times (PMC scale reference)")
     ap.add_argument("--staging", action="store_true",
                     help="also time the pinned-host round trip (default for workloads 3 and 4)")
+    ap.add_argument("--no-warm-staging", action="store_true",
+                    help="skip the second run of the pinned-host legs at the end of the process")
     ap.add_argument("--no-staging", action="store_true",
                     help="skip the pinned-host round trip, also for workloads 3 and 4")
     ap.add_argument("--no-append", action="store_true",
@@ -1313,6 +1316,18 @@ def summarize_kernel_pmc(kernel: str, command: str, csvs: list) -> str:
     return "\n".join(out) + "\n"
 
 
+def traffic_verdict(t: dict, alg: int) -> str:
+    """What the measured traffic says against the algorithmic bytes: within
+    0.1% of them, no re-reads and no partial-line writes; above that, the
+    excess of each direction (half of `alg` is read, half written)."""
+    if t["traffic_bytes_per_launch"] <= 1.001 * alg:
+        return "no re-reads, no partial-line writes (within 0.1%)."
+    rd = t["fetch_bytes_per_launch"] / (alg / 2) - 1
+    wr = t["write_bytes_per_launch"] / (alg / 2) - 1
+    return (f"{(t['traffic_bytes_per_launch'] / alg - 1) * 100:.2f}% above them; reads {rd * 100:+.2f}%, "
+            f"writes {wr * 100:+.2f}% against the bytes read and written once.")
+
+
 def pmc_markdown(traffic_json: str) -> str:
     """Markdown form of a --summarize-pmc result (the committed summary)."""
     t = _json(traffic_json)
@@ -1353,7 +1368,7 @@ def pmc_markdown(traffic_json: str) -> str:
         out += [f"Algorithmic bytes per launch: {alg} ({chunk} layers x {w.n_pages} pages x {w.shape.page_bytes} B, "
                 "read once and written once).",
                 f"Measured HBM traffic per launch: {t['traffic_bytes_per_launch']} B = "
-                f"{t['traffic_bytes_per_launch'] / alg:.5f} x algorithmic: no re-reads, no partial-line writes."]
+                f"{t['traffic_bytes_per_launch'] / alg:.5f} x algorithmic: {traffic_verdict(t, alg)}"]
     if rq:
         rdir = os.path.dirname(rq["rdreq_csv"])
         qdir = os.path.dirname(rq["wrreq_csv"])
@@ -1512,6 +1527,15 @@ def main():
                    for name in workloads.NAMES + workloads.SHARDS if name != w.name}
     if staging is None and early_staging:
         staging = next(iter(early_staging.values()))
+    # The same pinned-host legs again at the end, in a process that has run
+    # every other leg: a serving worker is never a fresh process.
+    staging_warm = None
+    if early_staging and not args.no_warm_staging:
+        staging_warm = {}
+        for name in early_staging:
+            settle = link_settle(dev)
+            staging_warm[name] = run_staging_leg(args, name, dev)
+            staging_warm[name]["link_probe"] = settle
 
     line = {
         "metric": METRIC,
@@ -1538,6 +1562,7 @@ def main():
         "append": append,
         "promote_4k": promote,
         "staging": staging,
+        "staging_warm": staging_warm,
         "dropin": dropin,
         "channel": channel,
         "cpu_baseline": cpu,
@@ -1554,6 +1579,13 @@ def main():
     if configs:
         line["configs_summary"] = {name: {"value": c["value"], "frac": c["frac_of_hbm_peak"],
                                           "verified": c.get("verified")} for name, c in configs.items()}
+    if early_staging:
+        # round trip GB/s per direction, first in the process and again at its end
+        line["staging_summary"] = {
+            name: {"fresh_gbs_per_direction": st["roundtrip_gbs_per_direction"], "fresh_verified": st.get("verified"),
+                   "warm_gbs_per_direction": (staging_warm or {}).get(name, {}).get("roundtrip_gbs_per_direction"),
+                   "warm_verified": (staging_warm or {}).get(name, {}).get("verified")}
+            for name, st in early_staging.items()}
     print(json.dumps(line), flush=True)
 
 
