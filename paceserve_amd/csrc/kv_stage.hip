@@ -4,17 +4,28 @@
 // (device->host, host->device), at <= ~64 GB/s per direction, i.e. two orders
 // of magnitude slower than the on-device pack/unpack.  The pipeline therefore
 // aims to keep both DMA directions busy at once and to hide pack/unpack under
-// them: layers are processed in chunks, and the round trip uses four streams
-//   caller stream : pack(c+1)
-//   D2H stream    : D2H(c)
+// them: layers are processed in chunks, and the round trip uses three streams
+//   caller stream : unpack(c-2), pack(c+1)
 //   H2D stream    : H2D(c-1)
-//   unpack stream : unpack(c-2)
+//   D2H stream    : D2H(c)
 // chunk c's device-to-host copy overlaps chunk c-1's host-to-device copy (the
 // two directions use separate DMA engines) and the kernels of neighbouring
-// chunks.  Unpacks have a stream of their own so that waiting for a chunk's
-// host-to-device copy never holds back the packs that feed the other
-// direction (measured: 1.5% faster than unpacking on the caller stream).
-// Events carry every dependency; nothing blocks the host.
+// chunks.  Events carry every dependency; nothing blocks the host.
+//
+// Enqueue order matters as much as the dependencies.  The runtime maps a
+// process's streams onto a few hardware queues (4 by default), shared in an
+// order that depends on every stream the process has used, and on a shared
+// queue a wait or an event record that follows a copy holds back everything
+// enqueued behind it until that copy finishes.  Enqueued chunk by chunk
+// (pack, D2H, H2D, unpack), the round trip ran at 47-48 GB/s per direction
+// with private queues but at 27.5 when the H2D stream shared the caller's
+// queue or the D2H stream's, since each pack or D2H copy then waited for the
+// previous H2D copy.  Each step therefore enqueues unpack(c-2) and pack(c+1)
+// first, then the waits of both copies, both copies, and both completion
+// records last, so anything a step enqueues is held back only until the
+// previous step's copies finish (measured: 45.6-47.2 GB/s per direction for
+// every way the three streams shared queues).  The one-way legs lead in the
+// same way: pack(c+1) before D2H(c), H2D(c+1) before unpack(c).
 //
 // Device slots are reused round-robin; before a slot is overwritten, the
 // stream that writes it waits for the event recorded after the last read of
@@ -99,10 +110,8 @@ struct pace_kv_stager {
   char* in_ring = nullptr;   // num_slots device slots written by H2D, read by unpack
   hipStream_t d2h = nullptr;
   hipStream_t h2d = nullptr;
-  hipStream_t unpack = nullptr;  // round trip: unpacks of the host chunks
   hipEvent_t start = nullptr;
   hipEvent_t d2h_done = nullptr;
-  hipEvent_t unpack_done = nullptr;
   std::vector<hipEvent_t> packed;    // out slot s filled (caller stream)
   std::vector<hipEvent_t> out_free;  // out slot s drained by D2H (D2H stream)
   std::vector<hipEvent_t> in_ready;  // in slot s filled by H2D (H2D stream)
@@ -133,10 +142,8 @@ void release(pace_kv_stager* s) {
   if (s->in_ring) (void)hipFree(s->in_ring);
   if (s->d2h) (void)hipStreamDestroy(s->d2h);
   if (s->h2d) (void)hipStreamDestroy(s->h2d);
-  if (s->unpack) (void)hipStreamDestroy(s->unpack);
   if (s->start) (void)hipEventDestroy(s->start);
   if (s->d2h_done) (void)hipEventDestroy(s->d2h_done);
-  if (s->unpack_done) (void)hipEventDestroy(s->unpack_done);
   destroy_events(s->packed);
   destroy_events(s->out_free);
   destroy_events(s->in_ready);
@@ -225,10 +232,8 @@ int pace_kv_stager_create(int64_t slot_bytes, int num_slots, pace_kv_stager** ou
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&s->in_ring), slot_bytes * num_slots);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->d2h, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->h2d, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->unpack, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&s->start, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&s->d2h_done, hipEventDisableTiming);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&s->unpack_done, hipEventDisableTiming);
   if (e == hipSuccess) e = make_events(s->packed, num_slots);
   if (e == hipSuccess) e = make_events(s->out_free, num_slots);
   if (e == hipSuccess) e = make_events(s->in_ready, num_slots);
@@ -247,12 +252,11 @@ int pace_kv_stager_destroy(pace_kv_stager* s) {
   // Work enqueued through the stager may still use its slots and streams.
   hipError_t e1 = hipStreamSynchronize(s->d2h);
   hipError_t e2 = hipStreamSynchronize(s->h2d);
-  hipError_t e3 = hipStreamSynchronize(s->unpack);
   for (hipEvent_t e : s->in_free) (void)hipEventSynchronize(e);
+  for (hipEvent_t e : s->packed) (void)hipEventSynchronize(e);
   release(s);
   if (e1 != hipSuccess) return hip_status(e1, "stager_destroy (D2H stream)");
-  if (e2 != hipSuccess) return hip_status(e2, "stager_destroy (H2D stream)");
-  return hip_status(e3, "stager_destroy (unpack stream)");
+  return hip_status(e2, "stager_destroy (H2D stream)");
 }
 
 int pace_kv_pack_to_host(pace_kv_stager* s, const void* const* src_layers, int num_layers,
@@ -265,17 +269,28 @@ int pace_kv_pack_to_host(pace_kv_stager* s, const void* const* src_layers, int n
   if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
   if (host_out == nullptr) return fail(PACE_KV_EINVAL, "pack_to_host: host_out is NULL");
   hipStream_t stream = static_cast<hipStream_t>(stream_);
-  for (int c = 0; c < p.num_chunks(); ++c) {
-    const int slot = c % s->num_slots;
-    PACE_HIP(hipStreamWaitEvent(stream, s->out_free[slot], 0), "wait out slot");
-    PACE_KV_TRY(pack_chunk(s, p, c, src_layers, pool_pages, page_ids, err_count, stream));
-    PACE_HIP(hipEventRecord(s->packed[slot], stream), "record packed");
-    PACE_HIP(hipStreamWaitEvent(s->d2h, s->packed[slot], 0), "wait packed");
-    PACE_HIP(hipMemcpyAsync(static_cast<char*>(host_out) + p.first(c) * p.layer_bytes,
-                            s->out_ring + slot * s->slot_bytes, p.count(c) * p.layer_bytes,
-                            hipMemcpyDeviceToHost, s->d2h),
-             "D2H copy");
-    PACE_HIP(hipEventRecord(s->out_free[slot], s->d2h), "record out_free");
+  const int chunks = p.num_chunks();
+  // Step i enqueues pack(i + 1), then the copy of chunk i: the copy's
+  // completion record, which holds back whatever follows it when the D2H
+  // stream shares the caller's hardware queue, then only delays pack(i + 2).
+  // pack(i + 1) refills the slot of chunk i + 1 - num_slots, whose copy was
+  // enqueued in an earlier step (num_slots >= 2).
+  for (int i = -1; i < chunks; ++i) {
+    if (i + 1 < chunks) {
+      const int slot = (i + 1) % s->num_slots;
+      PACE_HIP(hipStreamWaitEvent(stream, s->out_free[slot], 0), "wait out slot");
+      PACE_KV_TRY(pack_chunk(s, p, i + 1, src_layers, pool_pages, page_ids, err_count, stream));
+      PACE_HIP(hipEventRecord(s->packed[slot], stream), "record packed");
+    }
+    if (i >= 0) {
+      const int slot = i % s->num_slots;
+      PACE_HIP(hipStreamWaitEvent(s->d2h, s->packed[slot], 0), "wait packed");
+      PACE_HIP(hipMemcpyAsync(static_cast<char*>(host_out) + p.first(i) * p.layer_bytes,
+                              s->out_ring + slot * s->slot_bytes, p.count(i) * p.layer_bytes,
+                              hipMemcpyDeviceToHost, s->d2h),
+               "D2H copy");
+      PACE_HIP(hipEventRecord(s->out_free[slot], s->d2h), "record out_free");
+    }
   }
   PACE_HIP(hipEventRecord(s->d2h_done, s->d2h), "record d2h_done");
   PACE_HIP(hipStreamWaitEvent(stream, s->d2h_done, 0), "join D2H");
@@ -295,17 +310,28 @@ int pace_kv_unpack_from_host(pace_kv_stager* s, const void* host_in, void* const
   // The caller's earlier work (e.g. writes of host_in by a kernel) comes first.
   PACE_HIP(hipEventRecord(s->start, stream), "record start");
   PACE_HIP(hipStreamWaitEvent(s->h2d, s->start, 0), "wait start");
-  for (int c = 0; c < p.num_chunks(); ++c) {
-    const int slot = c % s->num_slots;
-    PACE_HIP(hipStreamWaitEvent(s->h2d, s->in_free[slot], 0), "wait in slot");
-    PACE_HIP(hipMemcpyAsync(s->in_ring + slot * s->slot_bytes,
-                            static_cast<const char*>(host_in) + p.first(c) * p.layer_bytes,
-                            p.count(c) * p.layer_bytes, hipMemcpyHostToDevice, s->h2d),
-             "H2D copy");
-    PACE_HIP(hipEventRecord(s->in_ready[slot], s->h2d), "record in_ready");
-    PACE_HIP(hipStreamWaitEvent(stream, s->in_ready[slot], 0), "wait in_ready");
-    PACE_KV_TRY(unpack_chunk(s, p, c, dst_layers, pool_pages, page_ids, err_count, stream));
-    PACE_HIP(hipEventRecord(s->in_free[slot], stream), "record in_free");
+  const int chunks = p.num_chunks();
+  // Step i enqueues the copy of chunk i + 1, then unpack(i), whose wait for
+  // chunk i's copy then holds back (on a shared hardware queue) only the copy
+  // of chunk i + 2.  That copy refills the slot of chunk i + 2 - num_slots,
+  // whose unpack was enqueued in an earlier step (num_slots >= 2).
+  for (int i = -1; i < chunks; ++i) {
+    if (i + 1 < chunks) {
+      const int c = i + 1;
+      const int slot = c % s->num_slots;
+      PACE_HIP(hipStreamWaitEvent(s->h2d, s->in_free[slot], 0), "wait in slot");
+      PACE_HIP(hipMemcpyAsync(s->in_ring + slot * s->slot_bytes,
+                              static_cast<const char*>(host_in) + p.first(c) * p.layer_bytes,
+                              p.count(c) * p.layer_bytes, hipMemcpyHostToDevice, s->h2d),
+               "H2D copy");
+      PACE_HIP(hipEventRecord(s->in_ready[slot], s->h2d), "record in_ready");
+    }
+    if (i >= 0) {
+      const int slot = i % s->num_slots;
+      PACE_HIP(hipStreamWaitEvent(stream, s->in_ready[slot], 0), "wait in_ready");
+      PACE_KV_TRY(unpack_chunk(s, p, i, dst_layers, pool_pages, page_ids, err_count, stream));
+      PACE_HIP(hipEventRecord(s->in_free[slot], stream), "record in_free");
+    }
   }
   return PACE_KV_OK;
 }
@@ -331,43 +357,99 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
   PACE_HIP(make_events(s->host_free, regions), "create host events");
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   char* host = static_cast<char*>(host_buf);
-  // The H2D copies and the unpacks come after the caller's earlier work.
-  PACE_HIP(hipEventRecord(s->start, stream), "record start");
-  PACE_HIP(hipStreamWaitEvent(s->h2d, s->start, 0), "wait start");
-  PACE_HIP(hipStreamWaitEvent(s->unpack, s->start, 0), "wait start");
-  // Every wait below names an event whose last record was enqueued in an
-  // earlier iteration (or an earlier call), so it orders against the right
-  // chunk: slot reuse waits for chunk c - num_slots, host region reuse for
-  // chunk c - regions.
-  for (int c = 0; c < chunks; ++c) {
-    const int slot = c % s->num_slots;
-    const int r = c % regions;
-    char* region = host + static_cast<int64_t>(r) * chunk_bytes;
-    const int64_t bytes = p.count(c) * p.layer_bytes;
+  const int S = s->num_slots;
+  // The stages of chunk c; each wait names an event whose record for the
+  // chunk it must follow is the latest one enqueued when the wait is.
+  auto pack = [&](int c) -> int {
+    const int slot = c % S;
     PACE_HIP(hipStreamWaitEvent(stream, s->out_free[slot], 0), "wait out slot");
     PACE_KV_TRY(pack_chunk(s, p, c, src_layers, src_pool_pages, src_ids, err_count, stream));
     PACE_HIP(hipEventRecord(s->packed[slot], stream), "record packed");
-    PACE_HIP(hipStreamWaitEvent(s->d2h, s->packed[slot], 0), "wait packed");
-    PACE_HIP(hipStreamWaitEvent(s->d2h, s->host_free[r], 0), "wait host region");
-    PACE_HIP(hipMemcpyAsync(region, s->out_ring + slot * s->slot_bytes, bytes,
+    return PACE_KV_OK;
+  };
+  auto d2h_wait = [&](int c) -> int {
+    PACE_HIP(hipStreamWaitEvent(s->d2h, s->packed[c % S], 0), "wait packed");
+    PACE_HIP(hipStreamWaitEvent(s->d2h, s->host_free[c % regions], 0), "wait host region");
+    return PACE_KV_OK;
+  };
+  auto d2h_copy = [&](int c) -> int {
+    PACE_HIP(hipMemcpyAsync(host + static_cast<int64_t>(c % regions) * chunk_bytes,
+                            s->out_ring + (c % S) * s->slot_bytes, p.count(c) * p.layer_bytes,
                             hipMemcpyDeviceToHost, s->d2h),
              "D2H copy");
-    PACE_HIP(hipEventRecord(s->out_free[slot], s->d2h), "record out_free");
-    PACE_HIP(hipEventRecord(s->host_full[r], s->d2h), "record host_full");
-    PACE_HIP(hipStreamWaitEvent(s->h2d, s->host_full[r], 0), "wait host_full");
-    PACE_HIP(hipStreamWaitEvent(s->h2d, s->in_free[slot], 0), "wait in slot");
-    PACE_HIP(hipMemcpyAsync(s->in_ring + slot * s->slot_bytes, region, bytes,
-                            hipMemcpyHostToDevice, s->h2d),
+    return PACE_KV_OK;
+  };
+  auto d2h_record = [&](int c) -> int {
+    PACE_HIP(hipEventRecord(s->out_free[c % S], s->d2h), "record out_free");
+    PACE_HIP(hipEventRecord(s->host_full[c % regions], s->d2h), "record host_full");
+    return PACE_KV_OK;
+  };
+  auto h2d_wait = [&](int c) -> int {
+    PACE_HIP(hipStreamWaitEvent(s->h2d, s->host_full[c % regions], 0), "wait host_full");
+    PACE_HIP(hipStreamWaitEvent(s->h2d, s->in_free[c % S], 0), "wait in slot");
+    return PACE_KV_OK;
+  };
+  auto h2d_copy = [&](int c) -> int {
+    PACE_HIP(hipMemcpyAsync(s->in_ring + (c % S) * s->slot_bytes,
+                            host + static_cast<int64_t>(c % regions) * chunk_bytes,
+                            p.count(c) * p.layer_bytes, hipMemcpyHostToDevice, s->h2d),
              "H2D copy");
-    PACE_HIP(hipEventRecord(s->in_ready[slot], s->h2d), "record in_ready");
-    PACE_HIP(hipEventRecord(s->host_free[r], s->h2d), "record host_free");
-    PACE_HIP(hipStreamWaitEvent(s->unpack, s->in_ready[slot], 0), "wait in_ready");
-    PACE_KV_TRY(unpack_chunk(s, p, c, dst_layers, dst_pool_pages, dst_ids, err_count, s->unpack));
-    PACE_HIP(hipEventRecord(s->in_free[slot], s->unpack), "record in_free");
+    return PACE_KV_OK;
+  };
+  auto h2d_record = [&](int c) -> int {
+    PACE_HIP(hipEventRecord(s->in_ready[c % S], s->h2d), "record in_ready");
+    PACE_HIP(hipEventRecord(s->host_free[c % regions], s->h2d), "record host_free");
+    return PACE_KV_OK;
+  };
+  auto unpack = [&](int c) -> int {
+    const int slot = c % S;
+    PACE_HIP(hipStreamWaitEvent(stream, s->in_ready[slot], 0), "wait in_ready");
+    PACE_KV_TRY(unpack_chunk(s, p, c, dst_layers, dst_pool_pages, dst_ids, err_count, stream));
+    PACE_HIP(hipEventRecord(s->in_free[slot], stream), "record in_free");
+    return PACE_KV_OK;
+  };
+  if (regions == 1) {
+    // One host region: each chunk's D2H copy must wait for the previous
+    // chunk's H2D copy to leave the region, so the stages run one chunk at
+    // a time.
+    for (int c = 0; c < chunks; ++c) {
+      PACE_KV_TRY(pack(c));
+      PACE_KV_TRY(d2h_wait(c));
+      PACE_KV_TRY(d2h_copy(c));
+      PACE_KV_TRY(d2h_record(c));
+      PACE_KV_TRY(h2d_wait(c));
+      PACE_KV_TRY(h2d_copy(c));
+      PACE_KV_TRY(h2d_record(c));
+      PACE_KV_TRY(unpack(c));
+    }
+    return PACE_KV_OK;
   }
-  // The caller's later work sees every destination page written.
-  PACE_HIP(hipEventRecord(s->unpack_done, s->unpack), "record unpack_done");
-  PACE_HIP(hipStreamWaitEvent(stream, s->unpack_done, 0), "join unpacks");
+  // Step i enqueues unpack(i-2) and pack(i+1) on `stream`, then both copy
+  // directions grouped: the waits of H2D(i-1) and D2H(i), the two copies,
+  // then their completion records.  The runtime may map the three streams
+  // onto shared hardware queues, where a wait or a record that follows a copy
+  // holds back everything enqueued behind it.  In this order everything a
+  // step enqueues is held back at most until the copies of the step before
+  // it finish, which is when the copies of this step are due to start, so the
+  // D2H and H2D copies overlap whichever queues the streams share.  Within a
+  // step, every wait names the record of the right chunk: unpack(i-2) follows
+  // H2D(i-2) (step i-1), pack(i+1) follows D2H(i+1-S) (step i+1-S <= i-1),
+  // H2D(i-1) follows D2H(i-1) (step i-1) and unpack(i-1-S) (step i+1-S), and
+  // D2H(i) follows pack(i) (step i-1) and H2D(i-regions) (step
+  // i-regions+1 <= i-1), which needs S >= 2 and regions >= 2.
+  for (int i = -1; i < chunks + 2; ++i) {
+    const bool h = i - 1 >= 0 && i - 1 < chunks;
+    const bool d = i >= 0 && i < chunks;
+    if (i - 2 >= 0 && i - 2 < chunks) PACE_KV_TRY(unpack(i - 2));
+    if (i + 1 < chunks) PACE_KV_TRY(pack(i + 1));
+    if (h) PACE_KV_TRY(h2d_wait(i - 1));
+    if (d) PACE_KV_TRY(d2h_wait(i));
+    if (h) PACE_KV_TRY(h2d_copy(i - 1));
+    if (d) PACE_KV_TRY(d2h_copy(i));
+    if (h) PACE_KV_TRY(h2d_record(i - 1));
+    if (d) PACE_KV_TRY(d2h_record(i));
+  }
+  // The last unpack is on `stream`: the caller's later work comes after it.
   return PACE_KV_OK;
 }
 
