@@ -130,15 +130,9 @@ __global__ __launch_bounds__(kThreads) void append_kernel(const AppendParams p) 
     kv = item & 1;
     chunk = 0;
   }
-  uint32_t page = 0, slot = 0;
-  if (!locate<FUSED>(p, i, &page, &slot)) {
-    if (kv == 0 && chunk == 0 && threadIdx.x == 0 && p.err != nullptr) atomicAdd(p.err, 1);
-    return;
-  }
+  // The row's loads depend on the token alone (always in range): they are
+  // issued before the index loads that place it, so their latencies overlap.
   const u32x4* src = reinterpret_cast<const u32x4*>((kv ? p.value : p.key) + static_cast<int64_t>(i) * p.token_stride);
-  const int64_t page_bytes = 2 * static_cast<int64_t>(p.page_size) * p.row_bytes;
-  u32x4* dst = reinterpret_cast<u32x4*>(p.cache + static_cast<int64_t>(page) * page_bytes +
-                                        (static_cast<int64_t>(kv) * p.page_size + slot) * p.row_bytes);
   const uint32_t first_vec = chunk * (V * kThreads) + threadIdx.x;
   u32x4 v[V];
 #pragma unroll
@@ -146,6 +140,14 @@ __global__ __launch_bounds__(kThreads) void append_kernel(const AppendParams p) 
     const uint32_t vec = first_vec + c * kThreads;
     if (!GUARD || vec < p.row_vecs) v[c] = __builtin_nontemporal_load(src + vec);
   }
+  uint32_t page = 0, slot = 0;
+  if (!locate<FUSED>(p, i, &page, &slot)) {
+    if (kv == 0 && chunk == 0 && threadIdx.x == 0 && p.err != nullptr) atomicAdd(p.err, 1);
+    return;
+  }
+  const int64_t page_bytes = 2 * static_cast<int64_t>(p.page_size) * p.row_bytes;
+  u32x4* dst = reinterpret_cast<u32x4*>(p.cache + static_cast<int64_t>(page) * page_bytes +
+                                        (static_cast<int64_t>(kv) * p.page_size + slot) * p.row_bytes);
 #pragma unroll
   for (int c = 0; c < V; ++c) {
     const uint32_t vec = first_vec + c * kThreads;
