@@ -582,12 +582,14 @@ def channel_sender(name: str) -> None:
     import torch
 
     from paceserve_amd import _native, workloads
+    from paceserve_amd.kv_transfer import ops
     from paceserve_amd.kv_transfer.channel import KVChannel
 
     _native.load()
     dev = torch.device("cuda", 0)
     w = workloads.get(workloads.PROMOTE)
-    src = w.src_pool(dev)
+    # the worker's cache as its KVhelper holds it (one pool, built once)
+    src = ops.PagedPool(w.src_pool(dev))
     torch.cuda.synchronize()
     ids = list(w.src_tables[0])
     with KVChannel.open(name, CHANNEL_THREADS, timeout=120) as ch:

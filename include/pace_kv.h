@@ -488,7 +488,10 @@ int pace_kv_channel_info(pace_kv_channel* channel, int64_t* slot_bytes,
 int pace_kv_channel_unlink(const char* name);
 
 /* Sends one message whose payload is packed from device pools:
- *   payload[l][j] = src_layers[l][page_ids[j]] (page_ids: device int32).
+ *   payload[l][j] = src_layers[l][page_ids[j]].
+ * page_ids: int32, in device memory, or in host memory (pageable or pinned)
+ * when n_pages <= 512: host ids travel in each pack's kernel arguments, so no
+ * upload precedes the first pack (more than 512 host ids: PACE_KV_ERANGE).
  * Packs run on `stream` after its earlier work.  Returns once every chunk is
  * in the ring (host-synchronous); *msg_id receives the message's id.  On the
  * GPU of a channel's device ring the chunks go into device slots. */
@@ -517,8 +520,9 @@ int pace_kv_channel_recv_header(pace_kv_channel* channel, void* meta,
                                 int64_t* page_bytes, uint64_t* msg_id,
                                 int timeout_ms);
 /* Receives the current message's payload into device pools:
- *   dst_layers[l][page_ids[j]] = payload[l][j] (page_ids: device int32,
- * distinct).  The shape must equal the header's.  Unpacks run on `stream`
+ *   dst_layers[l][page_ids[j]] = payload[l][j] (page_ids: int32, distinct,
+ * in device memory or, with n_pages <= 512, in host memory as for
+ * pace_kv_channel_send).  The shape must equal the header's.  Unpacks run on `stream`
  * after its earlier work; the call returns once every chunk has left the
  * ring, with the last unpacks still enqueued (a payload in device slots:
  * with every unpack finished, since a slot is released only then).  Ids outside [0, pool_pages)

@@ -50,6 +50,7 @@
 #include <time.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <condition_variable>
@@ -424,20 +425,29 @@ char* slot_data(pace_kv_channel* ch, uint32_t idx) {
 // A sender's wait (closed_first) fails on a closed channel even when cond()
 // holds, so nothing is published into a channel either side has closed; a
 // receiver's wait still takes records published before the sender closed.
+// The first kSpinUs of a wait poll without sleeping: the peer's next record
+// often follows within one chunk's copy time, and a futex wake-up would add
+// its own latency to every hand-over.
+constexpr int kSpinUs = 200;
+
 template <class Cond>
 int wait_for(pace_kv_channel* ch, std::atomic<uint32_t>* word, const ProcessId& peer, Cond cond,
              int timeout_ms, const char* what, bool closed_first = false) {
   using clock = std::chrono::steady_clock;
-  const auto deadline = clock::now() + std::chrono::milliseconds(timeout_ms < 0 ? 0 : timeout_ms);
+  const auto start = clock::now();
+  const auto deadline = start + std::chrono::milliseconds(timeout_ms < 0 ? 0 : timeout_ms);
+  const auto spin_end = std::min(deadline, start + std::chrono::microseconds(kSpinUs));
+  bool spinning = true;
   for (int spin = 0;; ++spin) {
     const uint32_t seen = word->load(std::memory_order_acquire);
     const bool closed = ch->ctl->closed.load(std::memory_order_acquire) != 0;
     if (!(closed && closed_first) && cond()) return PACE_KV_OK;
     if (closed)
       return fail(PACE_KV_ECLOSED, "channel %s: closed while waiting for %s", ch->name.c_str(), what);
-    if (spin < 256) {
+    if (spinning) {
       __builtin_ia32_pause();
-      continue;
+      if ((spin & 63) != 63 || clock::now() < spin_end) continue;
+      spinning = false;
     }
     if (role_gone(peer))
       return fail(PACE_KV_ECLOSED, "channel %s: the peer process %d exited while this side waited for %s",
@@ -728,11 +738,83 @@ void finish_chunk(pace_kv_channel* ch) {
   if (++ch->rx_next == ch->rx_chunks.num_chunks) ch->rx_active = false;
 }
 
+// ------------------------------------------------------------ page ids
+
+// The page ids of a send or a receive: device memory, or host memory of at
+// most PACE_KV_INLINE_IDS entries, which each launch carries in its kernel
+// arguments (no upload has to precede the first pack or unpack).
+struct PageIds {
+  const int32_t* ptr = nullptr;
+  bool host = false;
+};
+
+int classify_ids(const int32_t* ids, int64_t n, PageIds* out) {
+  out->ptr = ids;
+  hipPointerAttribute_t attr;
+  memset(&attr, 0, sizeof(attr));
+  const hipError_t e = hipPointerGetAttributes(&attr, ids);
+  if (e != hipSuccess) (void)hipGetLastError();  // pageable host memory is not known to the runtime
+  out->host = e != hipSuccess || (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged);
+  if (out->host && n > PACE_KV_INLINE_IDS)
+    return fail(PACE_KV_ERANGE, "channel: %lld page ids in host memory (at most %d; pass device ids)",
+                (long long)n, PACE_KV_INLINE_IDS);
+  return PACE_KV_OK;
+}
+
+// pack of pages [j0, j0 + nj) of layers [0, nl) into out[l][j - j0]
+// (layer stride `stride`), as pace_kv_pack.
+int pack_pages(const void* const* src_layers, int nl, int64_t pool_pages, const PageIds& ids, int64_t j0,
+               int64_t nj, int64_t page_bytes, char* out, int64_t stride, int32_t* err, hipStream_t stream) {
+  if (!ids.host)
+    return pace_kv_pack(src_layers, nl, pool_pages, ids.ptr + j0, nj, page_bytes, out, stride, err, stream);
+  std::vector<const char*> buf(static_cast<size_t>(nl));
+  pace_kv::buffer_layers(out, stride, nl, buf.data());
+  return pace_kv::launch_page_copy(
+      pace_kv::Side{reinterpret_cast<const char* const*>(src_layers), nullptr, pool_pages},
+      pace_kv::Side{buf.data(), nullptr, nj}, nl, nj, page_bytes, err, stream, ids.ptr + j0, nullptr,
+      pace_kv::StorePolicy::kPack);
+}
+
+// unpack of in[l][j - j0] into pages [j0, j0 + nj) of layers [0, nl), as
+// pace_kv_unpack.
+int unpack_pages(const char* in, int64_t stride, void* const* dst_layers, int nl, int64_t pool_pages,
+                 const PageIds& ids, int64_t j0, int64_t nj, int64_t page_bytes, int32_t* err, hipStream_t stream) {
+  if (!ids.host)
+    return pace_kv_unpack(in, stride, dst_layers, nl, pool_pages, ids.ptr + j0, nj, page_bytes, err, stream);
+  std::vector<const char*> buf(static_cast<size_t>(nl));
+  pace_kv::buffer_layers(in, stride, nl, buf.data());
+  return pace_kv::launch_page_copy(pace_kv::Side{buf.data(), nullptr, nj},
+                                   pace_kv::Side{reinterpret_cast<const char* const*>(dst_layers), nullptr,
+                                                 pool_pages},
+                                   nl, nj, page_bytes, err, stream, nullptr, ids.ptr + j0);
+}
+
 // ------------------------------------------------------------ device ring
+
+// PCI bus ids of this process's devices, looked up once per device: a
+// device ordinal names the same GPU for the whole process.
+constexpr int kMaxBusDevices = 64;
+std::mutex g_bus_mu;
+char g_bus_ids[kMaxBusDevices][kBusIdBytes];
+bool g_bus_known[kMaxBusDevices];
+
+int bus_id_of(int dev, char* bus) {
+  if (dev >= 0 && dev < kMaxBusDevices) {
+    std::lock_guard<std::mutex> lock(g_bus_mu);
+    if (!g_bus_known[dev]) {
+      PACE_KV_TRY(hip_status(hipDeviceGetPCIBusId(g_bus_ids[dev], kBusIdBytes, dev), "hipDeviceGetPCIBusId"));
+      g_bus_ids[dev][kBusIdBytes - 1] = '\0';
+      g_bus_known[dev] = true;
+    }
+    memcpy(bus, g_bus_ids[dev], kBusIdBytes);
+    return PACE_KV_OK;
+  }
+  return hip_status(hipDeviceGetPCIBusId(bus, kBusIdBytes, dev), "hipDeviceGetPCIBusId");
+}
 
 int current_bus_id(int* dev, char* bus) {
   PACE_KV_TRY(hip_status(hipGetDevice(dev), "hipGetDevice"));
-  return hip_status(hipDeviceGetPCIBusId(bus, kBusIdBytes, *dev), "hipDeviceGetPCIBusId");
+  return bus_id_of(*dev, bus);
 }
 
 // Whether the channel has a device ring on the current GPU.
@@ -754,7 +836,7 @@ void record_receiver_gpu(pace_kv_channel* ch) {
   uint64_t words[kBusIdBytes / 8] = {0};
   int dev = -1;
   char bus[kBusIdBytes] = {0};
-  if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetPCIBusId(bus, kBusIdBytes, dev) == hipSuccess) {
+  if (hipGetDevice(&dev) == hipSuccess && bus_id_of(dev, bus) == PACE_KV_OK) {
     bus[kBusIdBytes - 1] = '\0';
     memcpy(words, bus, sizeof(words));
   } else {
@@ -835,6 +917,26 @@ int ring_ready(pace_kv_channel* ch) {
   return make_slot_events(ch);
 }
 
+// A not-ready query is no error: it must not be left as the thread's last
+// HIP error for the caller's next error check to find.
+void clear_not_ready() {
+  if (hipPeekAtLastError() == hipErrorNotReady) (void)hipGetLastError();
+}
+
+// Waits for `e` by polling it, so that the host sees the completion within a
+// poll rather than after a blocking wait's wake-up (the hand-overs of the
+// device ring are on the path of every message).
+hipError_t poll_event(hipEvent_t e) {
+  for (;;) {
+    const hipError_t q = hipEventQuery(e);
+    if (q != hipErrorNotReady) {
+      clear_not_ready();
+      return q;
+    }
+    __builtin_ia32_pause();
+  }
+}
+
 char* dev_slot(pace_kv_channel* ch, uint32_t idx) {
   return ch->dev_ring + static_cast<int64_t>(idx) * ch->ctl->dev_slot_bytes;
 }
@@ -853,7 +955,7 @@ int acquire_slot_at(pace_kv_channel* ch, uint32_t pos, int timeout_ms, uint32_t*
 // Sender: publishes device chunk `c` of message `id` once its pack into slot
 // idx has finished.
 int publish_dev_chunk(pace_kv_channel* ch, uint64_t id, int64_t c, const Chunking::Chunk& k, uint32_t idx) {
-  PACE_KV_TRY(hip_status(hipEventSynchronize(ch->dev_packed[idx]), "channel pack into the device ring"));
+  PACE_KV_TRY(hip_status(poll_event(ch->dev_packed[idx]), "channel pack into the device ring"));
   SlotRecord& r = ch->ctl->slots[idx];
   r.kind = kDevData;
   r.chunk = static_cast<uint32_t>(c);
@@ -879,7 +981,7 @@ int abandon_device(pace_kv_channel* ch, uint64_t id, int rc, hipStream_t stream)
 // this thread waits for the previous one; at most one slot is reserved and
 // unpublished, so the receiver can always drain what precedes it.
 int send_device(pace_kv_channel* ch, const void* const* src_layers, int64_t pool_pages,
-                const int32_t* page_ids, const Chunking& k, uint64_t id, int timeout_ms, hipStream_t stream) {
+                const PageIds& page_ids, const Chunking& k, uint64_t id, int timeout_ms, hipStream_t stream) {
   const uint32_t first = ch->ctl->head.load(std::memory_order_relaxed);
   uint32_t prev = 0;
   for (int64_t c = 0; c < k.num_chunks; ++c) {
@@ -888,8 +990,8 @@ int send_device(pace_kv_channel* ch, const void* const* src_layers, int64_t pool
     int rc = acquire_slot_at(ch, first + static_cast<uint32_t>(c), timeout_ms, &idx);
     if (rc == PACE_KV_OK) {
       const int64_t stride = k.layers_per_chunk > 0 ? k.layer_bytes : ck.bytes;
-      rc = pace_kv_pack(src_layers + ck.layer, ck.nl, pool_pages, page_ids + ck.j0, ck.nj, k.page_bytes,
-                        dev_slot(ch, idx), stride, nullptr, stream);
+      rc = pack_pages(src_layers + ck.layer, ck.nl, pool_pages, page_ids, ck.j0, ck.nj, k.page_bytes,
+                      dev_slot(ch, idx), stride, nullptr, stream);
     }
     if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(ch->dev_packed[idx], stream), "channel send record");
     if (rc == PACE_KV_OK && c > 0) rc = publish_dev_chunk(ch, id, c - 1, k.at(c - 1), prev);
@@ -918,10 +1020,13 @@ int release_held(pace_kv_channel* ch, bool wait) {
   hipEvent_t e = ch->dev_unpacked[idx];
   int rc = PACE_KV_OK;
   if (wait) {
-    rc = hip_status(hipEventSynchronize(e), "channel unpack out of the device ring");
+    rc = hip_status(poll_event(e), "channel unpack out of the device ring");
   } else {
     const hipError_t q = hipEventQuery(e);
-    if (q == hipErrorNotReady) return PACE_KV_OK;  // still reading: keep the slot
+    if (q == hipErrorNotReady) {
+      clear_not_ready();
+      return PACE_KV_OK;  // still reading: keep the slot
+    }
     rc = hip_status(q, "channel unpack out of the device ring");
   }
   if (rc) return rc;
@@ -959,7 +1064,7 @@ int fail_rx_device(pace_kv_channel* ch, int rc, hipStream_t stream) {
 // queue does not drain between chunks; the sender, which reserves one slot
 // beyond the chunk it publishes, can then always publish the chunk waited for.
 // With two slots every unpack finishes before the next wait.
-int recv_device(pace_kv_channel* ch, void* const* dst_layers, int64_t pool_pages, const int32_t* page_ids,
+int recv_device(pace_kv_channel* ch, void* const* dst_layers, int64_t pool_pages, const PageIds& page_ids,
                 int32_t* err_count, int timeout_ms, hipStream_t stream) {
   PACE_KV_TRY(ring_ready(ch));
   const Chunking k = ch->rx_chunks;
@@ -983,8 +1088,8 @@ int recv_device(pace_kv_channel* ch, void* const* dst_layers, int64_t pool_pages
     int rc = next_chunk(ch, timeout_ms, &idx, &ck);
     if (rc) return release_all_held(ch, rc, stream);
     const int64_t stride = k.layers_per_chunk > 0 ? k.layer_bytes : ck.bytes;
-    rc = pace_kv_unpack(dev_slot(ch, idx), stride, dst_layers + ck.layer, ck.nl, pool_pages, page_ids + ck.j0,
-                        ck.nj, k.page_bytes, err_count, stream);
+    rc = unpack_pages(dev_slot(ch, idx), stride, dst_layers + ck.layer, ck.nl, pool_pages, page_ids, ck.j0,
+                      ck.nj, k.page_bytes, err_count, stream);
     if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(ch->dev_unpacked[idx], stream), "channel recv record");
     if (rc) return fail_rx_device(ch, rc, stream);
     ++ch->rx_held;
@@ -1224,8 +1329,10 @@ int pace_kv_channel_send(pace_kv_channel* ch, const void* const* src_layers, int
   PACE_KV_TRY(check_open(ch));
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   bool device = false;
+  PageIds ids;
   if (num_layers > 0 && n_pages > 0) {
     if (src_layers == nullptr || page_ids == nullptr) return fail(PACE_KV_EINVAL, "channel send: NULL argument");
+    PACE_KV_TRY(classify_ids(page_ids, n_pages, &ids));
     PACE_KV_TRY(device_ring_here(ch, &device));
     device = device && receiver_on_ring_gpu(ch);
   }
@@ -1238,7 +1345,7 @@ int pace_kv_channel_send(pace_kv_channel* ch, const void* const* src_layers, int
     PACE_KV_TRY(send_header(ch, num_layers, n_pages, page_bytes, meta, meta_bytes, timeout_ms, &id,
                             kDevicePayload));
     if (msg_id) *msg_id = id;
-    return send_device(ch, src_layers, pool_pages, page_ids, kd, id, timeout_ms, stream);
+    return send_device(ch, src_layers, pool_pages, ids, kd, id, timeout_ms, stream);
   }
   Chunking k;
   PACE_KV_TRY(make_chunking(num_layers, n_pages, page_bytes, ch->ctl->slot_bytes, &k));
@@ -1256,8 +1363,8 @@ int pace_kv_channel_send(pace_kv_channel* ch, const void* const* src_layers, int
       int rc = hip_status(hipStreamWaitEvent(stream, s.copied[b], 0), "channel send wait");
       if (rc == PACE_KV_OK) {
         const int64_t stride = k.layers_per_chunk > 0 ? k.layer_bytes : ck.bytes;
-        rc = pace_kv_pack(src_layers + ck.layer, ck.nl, pool_pages, page_ids + ck.j0, ck.nj, page_bytes,
-                          s.dev[b], stride, nullptr, stream);
+        rc = pack_pages(src_layers + ck.layer, ck.nl, pool_pages, ids, ck.j0, ck.nj, page_bytes, s.dev[b],
+                        stride, nullptr, stream);
       }
       if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(s.filled[b], stream), "channel send record");
       if (rc == PACE_KV_OK) rc = hip_status(hipStreamWaitEvent(s.copy, s.filled[b], 0), "channel send wait");
@@ -1353,9 +1460,10 @@ int pace_kv_channel_recv(pace_kv_channel* ch, void* const* dst_layers, int num_l
   std::lock_guard<std::mutex> lock(ch->recv_mu);
   PACE_KV_TRY(check_rx_shape(ch, num_layers, n_pages, page_bytes));
   if (dst_layers == nullptr || page_ids == nullptr) return fail(PACE_KV_EINVAL, "channel recv: NULL argument");
+  PageIds ids;
+  PACE_KV_TRY(classify_ids(page_ids, n_pages, &ids));
   if (ch->rx_device)
-    return recv_device(ch, dst_layers, pool_pages, page_ids, err_count, timeout_ms,
-                       static_cast<hipStream_t>(stream_));
+    return recv_device(ch, dst_layers, pool_pages, ids, err_count, timeout_ms, static_cast<hipStream_t>(stream_));
   PACE_KV_TRY(staging_ready(ch, ch->rx));
   const Chunking k = ch->rx_chunks;
   Staging& s = ch->rx;
@@ -1386,8 +1494,8 @@ int pace_kv_channel_recv(pace_kv_channel* ch, void* const* dst_layers, int num_l
     if (rc == PACE_KV_OK) rc = hip_status(hipStreamWaitEvent(stream, s.copied[b], 0), "channel recv wait");
     if (rc == PACE_KV_OK) {
       const int64_t stride = k.layers_per_chunk > 0 ? k.layer_bytes : ck.bytes;
-      rc = pace_kv_unpack(s.dev[b], stride, dst_layers + ck.layer, ck.nl, pool_pages, page_ids + ck.j0, ck.nj,
-                          page_bytes, err_count, stream);
+      rc = unpack_pages(s.dev[b], stride, dst_layers + ck.layer, ck.nl, pool_pages, ids, ck.j0, ck.nj,
+                        page_bytes, err_count, stream);
     }
     if (rc == PACE_KV_OK) rc = hip_status(hipEventRecord(s.drained[b], stream), "channel recv record");
     if (rc) {

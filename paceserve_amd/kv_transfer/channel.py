@@ -24,6 +24,7 @@ import threading
 from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
+import numpy as np
 import torch
 
 from .. import _native
@@ -48,6 +49,43 @@ class MessageHeader:
 
 def _ms(timeout: float) -> int:
     return max(0, min(int(timeout * 1000), 2**31 - 1))
+
+
+# Most page ids a send or receive passes in host memory: the library carries
+# them in each launch's kernel arguments, so no upload precedes the copies.
+HOST_IDS_MAX = 512
+
+
+def _ids(page_ids: ops.IdsLike, device: torch.device, distinct: bool = False):
+    """The page ids as the library takes them: a device tensor is used as it
+    is; host data of at most HOST_IDS_MAX ids becomes an int32 numpy array
+    (range-checked by the kernels, like device ids); longer host data is
+    uploaded (ops.device_ids).  distinct=True rejects repeated host ids."""
+    if isinstance(page_ids, torch.Tensor):
+        if page_ids.device.type == "cuda" or page_ids.numel() > HOST_IDS_MAX:
+            return ops.device_ids(page_ids, device, distinct)
+        arr = page_ids.to(torch.int32).contiguous().view(-1).numpy()
+    else:
+        if len(page_ids) > HOST_IDS_MAX:
+            return ops.device_ids(page_ids, device, distinct)
+        try:
+            arr = np.ascontiguousarray(page_ids, dtype=np.int32).reshape(-1)
+        except OverflowError as e:
+            raise ValueError("page ids outside the int32 range") from e
+    if distinct and arr.size > 1:
+        u, c = np.unique(arr, return_counts=True)
+        if (c > 1).any():
+            raise ValueError(f"destination page {int(u[c > 1][0])} appears more than once; destination page "
+                             "ids must be distinct")
+    return arr
+
+
+def _count(ids) -> int:
+    return int(ids.numel()) if isinstance(ids, torch.Tensor) else int(ids.size)
+
+
+def _ptr(ids) -> int:
+    return ids.data_ptr() if isinstance(ids, torch.Tensor) else ids.ctypes.data
 
 
 class KVChannel:
@@ -124,13 +162,13 @@ class KVChannel:
         Packs run on the current stream after its earlier work; the call
         returns when the whole payload is in the ring."""
         pool = ops.as_pool(src)
-        ids = ops.device_ids(page_ids, pool.device)
-        n = ids.numel()
+        ids = _ids(page_ids, pool.device)
+        n = _count(ids)
         out = ctypes.c_uint64()
         meta = bytes(meta)
         with torch.cuda.device(pool.device):
             _native.check(_native.load().pace_kv_channel_send(
-                self._require(), pool.table(), pool.num_layers, pool.num_pages, ids.data_ptr() if n else None,
+                self._require(), pool.table(), pool.num_layers, pool.num_pages, _ptr(ids) if n else None,
                 n, pool.page_bytes, meta, len(meta), _ms(timeout), ctypes.byref(out),
                 ops._stream_handle(pool.device)))
         return out.value
@@ -195,14 +233,14 @@ class KVChannel:
         stream; the last ones are still enqueued when the call returns."""
         h = self._current()
         pool = ops.as_pool(dst)
-        ids = ops.device_ids(page_ids, pool.device, distinct=True)
-        n = ids.numel()
+        ids = _ids(page_ids, pool.device, distinct=True)
+        n = _count(ids)
         if (pool.num_layers, n, pool.page_bytes) != (h.num_layers, h.n_pages, h.page_bytes):
             raise ValueError(f"message {h.msg_id} holds {h.num_layers} layers x {h.n_pages} pages x "
                              f"{h.page_bytes} B; the destination is {pool.num_layers} x {n} x {pool.page_bytes} B")
         with torch.cuda.device(pool.device):
             _native.check(_native.load().pace_kv_channel_recv(
-                self._require(), pool.table(), pool.num_layers, pool.num_pages, ids.data_ptr(), n,
+                self._require(), pool.table(), pool.num_layers, pool.num_pages, _ptr(ids), n,
                 pool.page_bytes, ops._err_ptr(err), _ms(timeout), ops._stream_handle(pool.device)))
             ev = torch.cuda.Event()
             ev.record(torch.cuda.current_stream(pool.device))

@@ -16,6 +16,7 @@ import torch
 
 from paceserve_amd import workloads
 from paceserve_amd.core.sequence import Sequence
+from paceserve_amd.kv_transfer import ops
 from paceserve_amd.kv_transfer.channel import KVChannel, KVref
 from paceserve_amd.kv_transfer.kv_utils import KVhelper
 from paceserve_amd.kv_transfer.worker import KVStatus, KVWorker, WorkerSequenceManager
@@ -655,14 +656,19 @@ def test_random_channel_messages(gpu, seed):
         d_ids = rng.permutation(pages)[:n].tolist()
         msgs.append((s_ids, d_ids))
 
+    # page ids alternate between host lists (carried in the kernel arguments)
+    # and device tensors, on both sides
+    def as_ids(ids, i):
+        return ids if (i + seed) % 2 == 0 else torch.tensor(ids, dtype=torch.int32, device=gpu)
+
     def send(tx):
-        return [tx.send(src, s, f"m{i}".encode(), timeout=30) for i, (s, _) in enumerate(msgs)]
+        return [tx.send(src, as_ids(s, i), f"m{i}".encode(), timeout=30) for i, (s, _) in enumerate(msgs)]
 
     def recv(rx):
         for i, (_, d) in enumerate(msgs):
             h = rx.recv_header(timeout=30)
             assert (h.meta, h.num_layers, h.n_pages) == (f"m{i}".encode(), L, n)
-            rx.recv(dst, d, timeout=30)
+            rx.recv(dst, as_ids(d, i + 1), timeout=30)
         torch.cuda.synchronize()
 
     if ring == "device":
@@ -677,3 +683,40 @@ def test_random_channel_messages(gpu, seed):
             want[l][di] = words(src[l])[si]
     for l in range(L):
         assert torch.equal(words(dst[l]), want[l]), f"layer {l}"
+
+
+@pytest.mark.parametrize("ring", RINGS)
+def test_host_page_ids_beyond_the_inline_limit(gpu, ring):
+    """Through the C ABI, more than 512 page ids in host memory are refused
+    with PACE_KV_ERANGE before anything is sent; through KVChannel the same
+    ids go up to the device instead, and arrive."""
+    from paceserve_amd import _native
+
+    L, pages, shape, n = 2, 700, (2, 16, 1, 64), 600
+    src = rand_pool(L, pages, shape, torch.float16, gpu, 50)
+    dst = rand_pool(L, pages, shape, torch.float16, gpu, 51)
+    before = [d.clone() for d in dst]
+    s_ids = np.random.default_rng(50).permutation(pages)[:n].tolist()
+    d_ids = np.random.default_rng(51).permutation(pages)[:n].tolist()
+    refused = []
+
+    def send(tx):
+        lib = _native.load()
+        pool = ops.PagedPool(src)
+        host = np.ascontiguousarray(s_ids, dtype=np.int32)
+        rc = lib.pace_kv_channel_send(tx._require(), pool.table(), L, pages, host.ctypes.data, n, pool.page_bytes,
+                                      None, 0, 1000, None, torch.cuda.current_stream(gpu).cuda_stream)
+        refused.append((rc, lib.pace_kv_last_error()))
+        tx.send(src, s_ids, b"m", timeout=30)               # uploaded by KVChannel
+
+    def recv(rx):
+        h = rx.recv_header(timeout=30)
+        assert (h.meta, h.n_pages) == (b"m", n)
+        rx.recv(dst, d_ids, timeout=30)
+        torch.cuda.synchronize()
+
+    run_pair(1 << 20, 4, send, recv, RINGS[ring])
+    assert refused[0][0] == _native.PACE_KV_ERANGE and b"at most 512" in refused[0][1], refused
+    bad = workloads.migration_mismatch(src, dst, torch.tensor(s_ids, device=gpu), torch.tensor(d_ids, device=gpu),
+                                       before)
+    assert bad is None, bad
