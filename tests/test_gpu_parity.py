@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from oracle import kv_oracle as orc
-from paceserve_amd import _native
+from paceserve_amd import _native, workloads
 from paceserve_amd.kv_transfer import ops
 
 pytestmark = pytest.mark.gpu
@@ -309,7 +309,40 @@ def test_concurrent_host_threads_on_their_own_streams(gpu):
             assert same(dst[l].index_select(0, di), src[l].index_select(0, si))
 
 
-@pytest.mark.parametrize("seed", range(8))
+# (slots, host ring regions, layers, layers per chunk): the round trip's
+# enqueue order needs two slots and two regions, and runs one chunk at a time
+# with a one-region ring; a two-slot stager with many chunks exercises every
+# wait of the order at its tightest.
+ROUNDTRIP_EDGES = [(2, 2, 12, 1), (2, 12, 12, 1), (3, 1, 6, 1), (5, 3, 13, 2), (2, 2, 2, 1), (4, 1, 1, 1)]
+
+
+@pytest.mark.parametrize("slots,regions,L,k", ROUNDTRIP_EDGES)
+def test_roundtrip_enqueue_order_edges(gpu, slots, regions, L, k):
+    """pace_kv_roundtrip at the edges of its enqueue order, three calls in a
+    row on one stager (the later calls wait on events the earlier ones
+    recorded) with a different host ring and batch each time: every layer of
+    the destination equals torch's scatter of torch's gather."""
+    print(f"roundtrip edges: slots={slots} regions={regions} L={L} k={k}", flush=True)
+    shape, pages = (2, 16, 2, 64), 40
+    page_bytes = int(np.prod(shape)) * 2
+    src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 300 + L)
+    rng = np.random.default_rng(300 + slots * 10 + regions)
+    with ops.Stager(-(-(k * pages * page_bytes) // 256) * 256, slots) as st:
+        for rep in range(3):
+            n = int(rng.integers(1, pages + 1))
+            s_ids = rng.permutation(pages)[:n].tolist()
+            d_ids = rng.permutation(pages)[:n].tolist()
+            dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 400 + rep)
+            before = [d.clone() for d in dst]
+            ring = torch.empty(regions * k * n * page_bytes, dtype=torch.uint8, pin_memory=True)
+            st.roundtrip(src, s_ids, dst, d_ids, ring, k)
+            torch.cuda.current_stream().synchronize()
+            bad = workloads.migration_mismatch(src, dst, torch.tensor(s_ids, device=gpu),
+                                               torch.tensor(d_ids, device=gpu), before)
+            assert bad is None, f"rep {rep}: {bad}"
+
+
+@pytest.mark.parametrize("seed", range(16))
 def test_random_staging_matches_torch(gpu, seed):
     """Seeded random pinned-host legs through one stager: layer counts on both
     sides of the 64-layer launch split, pages of 64 B to 64 KiB (whole and
