@@ -516,3 +516,25 @@ def test_host_channel_reports_no_device_ring():
         assert ch.device_ring() == (0, False)
     finally:
         ch.close()
+
+
+def test_host_page_ids_become_int32_arrays_for_the_kernel_arguments():
+    """Block tables of at most 512 ids in host memory reach the library as
+    int32 numpy arrays (the kernels carry them in their arguments and skip
+    out-of-pool ids, as they do device ids); repeated destination ids and
+    values beyond int32 are refused before any device call."""
+    from paceserve_amd.kv_transfer import channel as chan
+
+    dev = torch.device("cpu")              # not touched on the host path
+    ids = chan._ids([5, 3, -1, 2**31 - 1], dev)
+    assert isinstance(ids, np.ndarray) and ids.dtype == np.int32 and ids.tolist() == [5, 3, -1, 2**31 - 1]
+    assert chan._count(ids) == 4 and chan._ptr(ids) == ids.ctypes.data
+    t = chan._ids(torch.tensor([7, 1, 4], dtype=torch.int64), dev)
+    assert t.dtype == np.int32 and t.tolist() == [7, 1, 4]
+    assert chan._ids(list(range(chan.HOST_IDS_MAX)), dev).size == chan.HOST_IDS_MAX
+    with pytest.raises(ValueError, match="appears more than once"):
+        chan._ids([3, 9, 3], dev, distinct=True)
+    assert chan._ids([3, 9, 3], dev).tolist() == [3, 9, 3]      # source ids may repeat
+    with pytest.raises(ValueError, match="int32"):
+        chan._ids([2**31], dev)
+    assert chan._count(chan._ids([], dev)) == 0
