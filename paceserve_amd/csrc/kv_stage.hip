@@ -112,6 +112,7 @@ struct pace_kv_stager {
   hipStream_t h2d = nullptr;
   hipEvent_t start = nullptr;
   hipEvent_t d2h_done = nullptr;
+  hipEvent_t h2d_done = nullptr;  // the last round trip's last H2D copy
   std::vector<hipEvent_t> packed;    // out slot s filled (caller stream)
   std::vector<hipEvent_t> out_free;  // out slot s drained by D2H (D2H stream)
   std::vector<hipEvent_t> in_ready;  // in slot s filled by H2D (H2D stream)
@@ -144,6 +145,7 @@ void release(pace_kv_stager* s) {
   if (s->h2d) (void)hipStreamDestroy(s->h2d);
   if (s->start) (void)hipEventDestroy(s->start);
   if (s->d2h_done) (void)hipEventDestroy(s->d2h_done);
+  if (s->h2d_done) (void)hipEventDestroy(s->h2d_done);
   destroy_events(s->packed);
   destroy_events(s->out_free);
   destroy_events(s->in_ready);
@@ -234,6 +236,7 @@ int pace_kv_stager_create(int64_t slot_bytes, int num_slots, pace_kv_stager** ou
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->h2d, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&s->start, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&s->d2h_done, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&s->h2d_done, hipEventDisableTiming);
   if (e == hipSuccess) e = make_events(s->packed, num_slots);
   if (e == hipSuccess) e = make_events(s->out_free, num_slots);
   if (e == hipSuccess) e = make_events(s->in_ready, num_slots);
@@ -358,6 +361,11 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   char* host = static_cast<char*>(host_buf);
   const int S = s->num_slots;
+  // A region's events order its reuse within a call and between calls of one
+  // chunk size; a call with another chunk size (or host buffer) carves other
+  // regions, so its first D2H copy waits for the previous call's last H2D
+  // copy to have read the host buffer.
+  PACE_HIP(hipStreamWaitEvent(s->d2h, s->h2d_done, 0), "wait previous round trip");
   // The stages of chunk c; each wait names an event whose record for the
   // chunk it must follow is the latest one enqueued when the wait is.
   auto pack = [&](int c) -> int {
@@ -422,6 +430,7 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
       PACE_KV_TRY(h2d_record(c));
       PACE_KV_TRY(unpack(c));
     }
+    PACE_HIP(hipEventRecord(s->h2d_done, s->h2d), "record h2d_done");
     return PACE_KV_OK;
   }
   // Step i enqueues unpack(i-2) and pack(i+1) on `stream`, then both copy
@@ -449,6 +458,7 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
     if (h) PACE_KV_TRY(h2d_record(i - 1));
     if (d) PACE_KV_TRY(d2h_record(i));
   }
+  PACE_HIP(hipEventRecord(s->h2d_done, s->h2d), "record h2d_done");
   // The last unpack is on `stream`: the caller's later work comes after it.
   return PACE_KV_OK;
 }

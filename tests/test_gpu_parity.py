@@ -342,6 +342,35 @@ def test_roundtrip_enqueue_order_edges(gpu, slots, regions, L, k):
             assert bad is None, f"rep {rep}: {bad}"
 
 
+def test_roundtrips_on_two_streams_share_one_host_buffer(gpu):
+    """Two round trips through one stager and one pinned host buffer,
+    enqueued back to back on two streams with no synchronisation between
+    them and with different chunk sizes (so their host regions overlap
+    differently): the second call's device-to-host copies wait for the
+    first call's host-to-device copies, and both destinations are exact."""
+    L, pages, shape = 8, 48, (2, 16, 2, 64)
+    page_bytes = int(np.prod(shape)) * 2
+    src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 500)
+    dsts = [rand_pool(L, pages, shape, torch.bfloat16, gpu, 501 + i) for i in range(2)]
+    befores = [[d.clone() for d in dst] for dst in dsts]
+    rng = np.random.default_rng(500)
+    n = 40
+    s_ids = [rng.permutation(pages)[:n].tolist() for _ in range(2)]
+    d_ids = [rng.permutation(pages)[:n].tolist() for _ in range(2)]
+    host = torch.empty(4 * n * page_bytes, dtype=torch.uint8, pin_memory=True)   # 4 one-layer regions, 2 two-layer
+    streams = [torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)]
+    torch.cuda.synchronize()
+    with ops.Stager(2 * n * page_bytes, 3) as st:
+        for i, k in enumerate((1, 2)):
+            with torch.cuda.stream(streams[i]):
+                st.roundtrip(src, s_ids[i], dsts[i], d_ids[i], host, k)
+        torch.cuda.synchronize()
+    for i in range(2):
+        bad = workloads.migration_mismatch(src, dsts[i], torch.tensor(s_ids[i], device=gpu),
+                                           torch.tensor(d_ids[i], device=gpu), befores[i])
+        assert bad is None, f"call {i}: {bad}"
+
+
 @pytest.mark.parametrize("seed", range(16))
 def test_random_staging_matches_torch(gpu, seed):
     """Seeded random pinned-host legs through one stager: layer counts on both
