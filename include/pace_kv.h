@@ -233,8 +233,8 @@ int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers,
 
 /*
  * Full host round trip in one pipeline: pack(c) -> D2H(c) -> H2D(c) ->
- * unpack(c) per layer chunk, with pack(c+1), D2H(c), H2D(c-1) and
- * unpack(c-2) in flight together (D2H and H2D run on two streams of the
+ * unpack(c) per layer chunk, with pack(c+1), D2H(c), H2D(c-1) and the
+ * unpacks of earlier chunks in flight together (D2H and H2D run on two streams of the
  * stager's own; packs and unpacks run on `stream`, so `stream`'s later work
  * comes after the last unpack).  The copies overlap however the runtime maps
  * these streams onto its hardware queues.
