@@ -71,7 +71,10 @@ def test_mixed_prefill_and_decode_batch_matches_oracle(gpu, dtype, H, D, P, R):
     append_indptr = np.concatenate([[0], np.cumsum(app)])
     nnz = int(append_indptr[-1])
     wt = WORD[dtype]
-    raw = lambda shape: torch.from_numpy(rng.integers(-2 ** 7, 2 ** 7, shape).astype(np.int8)).to(gpu)
+    # int8 words of each tensor, copied into a fresh tensor so that an empty
+    # batch (no new tokens) still has the strides a dtype view needs
+    raw = lambda shape: torch.empty(shape, dtype=torch.int8, device=gpu).copy_(
+        torch.from_numpy(rng.integers(-2 ** 7, 2 ** 7, shape).astype(np.int8)))
     k = raw((nnz, H, D * torch.empty(0, dtype=dtype).element_size())).view(dtype).view(nnz, H, D)
     v = raw((nnz, H, D * torch.empty(0, dtype=dtype).element_size())).view(dtype).view(nnz, H, D)
     cache = raw((NP, 2, P, H, D * torch.empty(0, dtype=dtype).element_size())).view(dtype).view(NP, 2, P, H, D)
@@ -191,7 +194,7 @@ def test_append_of_70000_tokens(gpu):
     assert torch.equal(words(cache[first, :, :5]), words(before[first, :, :5]))
 
 
-@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("seed", list(range(6)) + [283])   # seed 283: one request, no new tokens
 def test_random_appends_match_numpy(gpu, seed):
     """Seeded random batches through both forms: 1-1000 requests (the fused
     form's request search takes more than one round of 256 past 256
@@ -216,7 +219,10 @@ def test_random_appends_match_numpy(gpu, seed):
     append_indptr = np.concatenate([[0], np.cumsum(app)])
     nnz = int(append_indptr[-1])
     print(f"random append seed {seed}: R={R} P={P} H={H} D={D} {dtype} nnz={nnz} pages={NP}", flush=True)
-    raw = lambda shape: torch.from_numpy(rng.integers(-2 ** 7, 2 ** 7, shape).astype(np.int8)).to(gpu)
+    # int8 words of each tensor, copied into a fresh tensor so that an empty
+    # batch (no new tokens) still has the strides a dtype view needs
+    raw = lambda shape: torch.empty(shape, dtype=torch.int8, device=gpu).copy_(
+        torch.from_numpy(rng.integers(-2 ** 7, 2 ** 7, shape).astype(np.int8)))
     k = raw((nnz, H, D * esz)).view(dtype).view(nnz, H, D)
     v = raw((nnz, H, D * esz)).view(dtype).view(nnz, H, D)
     cache = raw((NP, 2, P, H, D * esz)).view(dtype).view(NP, 2, P, H, D)
