@@ -768,7 +768,7 @@ def run_staging(w, dev, src, dst, s_ids, d_ids, reps: int = 3):
 
     out = {"layers_per_chunk": k, "chunks": chunks, "chunk_bytes": chunk, "host_ring_bytes": host_bytes,
            "pcie_peak_gbs_per_direction": 64.0}
-    with ops.Stager(-(-chunk // 256) * 256, 3, dev) as st:
+    with ops.Stager(-(-chunk // 256) * 256, kv_utils.ROUNDTRIP_SLOTS, dev) as st:
         t_rt = timed(lambda: st.roundtrip(src, s_ids, dst, d_ids, host, k))
         out["roundtrip_ms"] = round(t_rt * 1e3, 3)
         out["roundtrip_gbs_per_direction"] = round(w.payload_bytes / t_rt / 1e9, 2)

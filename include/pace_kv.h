@@ -148,9 +148,9 @@ int pace_kv_swap_in(const void* const* host_layers, int64_t host_pool_pages,
 
 /*
  * A stager owns two rings of device slots (one feeding device-to-host copies,
- * one fed by host-to-device copies), three side streams (D2H copies, H2D
- * copies and the round trip's unpacks; default priority) and the events that
- * order them against the caller's stream.
+ * one fed by host-to-device copies), three side streams created one after
+ * another (the round trip's packs and unpacks, D2H copies, H2D copies; default
+ * priority) and the events that order them against the caller's stream.
  * Each slot holds slot_bytes; a layer chunk of k layers needs
  * k * n_pages * page_bytes <= slot_bytes.
  */
@@ -234,10 +234,14 @@ int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers,
 /*
  * Full host round trip in one pipeline: pack(c) -> D2H(c) -> H2D(c) ->
  * unpack(c) per layer chunk, with pack(c+1), D2H(c), H2D(c-1) and the
- * unpacks of earlier chunks in flight together (D2H and H2D run on two streams of the
- * stager's own; packs and unpacks run on `stream`, so `stream`'s later work
- * comes after the last unpack).  The copies overlap however the runtime maps
- * these streams onto its hardware queues.
+ * unpacks of earlier chunks in flight together.  Packs, D2H copies and H2D
+ * copies plus unpacks run on three streams of the stager's own: the packs
+ * start after the work enqueued on `stream` before the call, and `stream`
+ * waits for everything the call enqueued, so `stream`'s later work comes
+ * after the last unpack (also when the call fails part-way).  The copies
+ * overlap however the runtime maps these streams onto its hardware queues.
+ * Calls on one stager run their packs and unpacks in call order, whichever
+ * `stream` each names.
  * host_buf holds host_bytes of host memory used as a ring of chunk-sized
  * regions (host_bytes >= one chunk; pass the full payload to keep a complete
  * host copy, as the reference's KVobj does).

@@ -5,12 +5,13 @@
 // of magnitude slower than the on-device pack/unpack.  The pipeline therefore
 // aims to keep both DMA directions busy at once and to hide pack/unpack under
 // them: layers are processed in chunks, and the round trip uses three streams
-//   caller stream : unpack(c-S), pack(c+1)   (S = the stager's slots)
-//   H2D stream    : H2D(c-1)
-//   D2H stream    : D2H(c)
-// chunk c's device-to-host copy overlaps chunk c-1's host-to-device copy (the
-// two directions use separate DMA engines) and the kernels of neighbouring
-// chunks.  Events carry every dependency; nothing blocks the host.
+//   work stream : unpack(c-S), pack(c+1)   (S = the stager's slots)
+//   H2D stream  : H2D(c-1)
+//   D2H stream  : D2H(c)
+// chunk c's device-to-host copy overlaps chunk c-1's host-to-device copy and
+// the kernels of neighbouring chunks.  Events carry every dependency; nothing
+// blocks the host.  The work stream waits for the caller's stream at the start
+// of a call, and the caller's stream waits for it at the end.
 //
 // Enqueue order matters as much as the dependencies.  The runtime maps a
 // process's streams onto a few hardware queues (4 by default), shared in an
@@ -26,6 +27,14 @@
 // previous step's copies finish (measured: 45.6-47.2 GB/s per direction for
 // every way the three streams shared queues).  The one-way legs lead in the
 // same way: pack(c+1) before D2H(c), H2D(c+1) before unpack(c).
+//
+// In a torch process the HIP runtime is the one torch ships, and it carries
+// each D2H copy as a blit kernel whose waves hold the CUs until the copy
+// drains, so packs and unpacks run only between those copies.  Small requests
+// (4-8 chunks) suffer most from that: with the caller's stream as the kernel
+// stream they ran at 29-38 GB/s per direction depending on which hardware
+// queue that stream shared, and on the stager's own work stream, created next
+// to its copy streams, at 37-38; larger requests gained 1-2 GB/s.
 //
 // Device slots are reused round-robin; before a slot is overwritten, the
 // stream that writes it waits for the event recorded after the last read of
@@ -108,8 +117,11 @@ struct pace_kv_stager {
   int num_slots = 0;
   char* out_ring = nullptr;  // num_slots device slots written by pack, read by D2H
   char* in_ring = nullptr;   // num_slots device slots written by H2D, read by unpack
+  hipStream_t work = nullptr;
   hipStream_t d2h = nullptr;
   hipStream_t h2d = nullptr;
+  hipEvent_t work_start = nullptr;
+  hipEvent_t work_done = nullptr;
   hipEvent_t start = nullptr;
   hipEvent_t d2h_done = nullptr;
   hipEvent_t h2d_done = nullptr;  // the last round trip's last H2D copy
@@ -141,6 +153,9 @@ void destroy_events(std::vector<hipEvent_t>& v) {
 void release(pace_kv_stager* s) {
   if (s->out_ring) (void)hipFree(s->out_ring);
   if (s->in_ring) (void)hipFree(s->in_ring);
+  if (s->work) (void)hipStreamDestroy(s->work);
+  if (s->work_start) (void)hipEventDestroy(s->work_start);
+  if (s->work_done) (void)hipEventDestroy(s->work_done);
   if (s->d2h) (void)hipStreamDestroy(s->d2h);
   if (s->h2d) (void)hipStreamDestroy(s->h2d);
   if (s->start) (void)hipEventDestroy(s->start);
@@ -216,6 +231,25 @@ int unpack_chunk(pace_kv_stager* s, const ChunkPlan& p, int c, void* const* dst_
                         p.n_pages, p.page_bytes, err, stream);
 }
 
+// Makes `caller` wait for everything enqueued on the stager's work stream so
+// far: now() on the success path (reporting a failure), the destructor on an
+// early error return (best effort: the call is failing already).
+struct WorkJoin {
+  pace_kv_stager* s;
+  hipStream_t caller;
+  bool joined = false;
+  int now() {
+    joined = true;
+    PACE_HIP(hipEventRecord(s->work_done, s->work), "record work_done");
+    PACE_HIP(hipStreamWaitEvent(caller, s->work_done, 0), "wait work_done");
+    return PACE_KV_OK;
+  }
+  ~WorkJoin() {
+    if (!joined && hipEventRecord(s->work_done, s->work) == hipSuccess)
+      (void)hipStreamWaitEvent(caller, s->work_done, 0);
+  }
+};
+
 }  // namespace
 
 extern "C" {
@@ -232,8 +266,11 @@ int pace_kv_stager_create(int64_t slot_bytes, int num_slots, pace_kv_stager** ou
   hipError_t e = hipGetDevice(&s->device);
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&s->out_ring), slot_bytes * num_slots);
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&s->in_ring), slot_bytes * num_slots);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->work, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->d2h, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->h2d, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&s->work_start, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&s->work_done, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&s->start, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&s->d2h_done, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&s->h2d_done, hipEventDisableTiming);
@@ -253,6 +290,7 @@ int pace_kv_stager_create(int64_t slot_bytes, int num_slots, pace_kv_stager** ou
 int pace_kv_stager_destroy(pace_kv_stager* s) {
   if (s == nullptr) return PACE_KV_OK;
   // Work enqueued through the stager may still use its slots and streams.
+  (void)hipStreamSynchronize(s->work);
   hipError_t e1 = hipStreamSynchronize(s->d2h);
   hipError_t e2 = hipStreamSynchronize(s->h2d);
   for (hipEvent_t e : s->in_free) (void)hipEventSynchronize(e);
@@ -358,7 +396,15 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
   const int regions = regions64 < chunks ? static_cast<int>(regions64) : chunks;
   PACE_HIP(make_events(s->host_full, regions), "create host events");
   PACE_HIP(make_events(s->host_free, regions), "create host events");
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  // Packs and unpacks run on the stager's work stream, created together with
+  // its two copy streams (see the file comment); the work stream starts after
+  // the caller's earlier work, and the caller's stream waits for everything
+  // the call enqueued on it, on every return path.
+  hipStream_t caller = static_cast<hipStream_t>(stream_);
+  hipStream_t stream = s->work;
+  WorkJoin join{s, caller};
+  PACE_HIP(hipEventRecord(s->work_start, caller), "record work_start");
+  PACE_HIP(hipStreamWaitEvent(stream, s->work_start, 0), "wait work_start");
   char* host = static_cast<char*>(host_buf);
   const int S = s->num_slots;
   // A region's events order its reuse within a call and between calls of one
@@ -431,7 +477,7 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
       PACE_KV_TRY(unpack(c));
     }
     PACE_HIP(hipEventRecord(s->h2d_done, s->h2d), "record h2d_done");
-    return PACE_KV_OK;
+    return join.now();
   }
   // Step i enqueues unpack(i-S) and pack(i+1) on `stream`, then both copy
   // directions grouped: the waits of H2D(i-1) and D2H(i), the two copies,
@@ -462,8 +508,9 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
     if (d) PACE_KV_TRY(d2h_record(i));
   }
   PACE_HIP(hipEventRecord(s->h2d_done, s->h2d), "record h2d_done");
-  // The last unpack is on `stream`: the caller's later work comes after it.
-  return PACE_KV_OK;
+  // The last unpack is on the work stream: the caller's later work comes
+  // after it.
+  return join.now();
 }
 
 int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers, int64_t pool_pages,

@@ -37,6 +37,15 @@ from . import ops
 # request into more chunks gains nothing.
 STAGE_CHUNK_BYTES = 64 << 20
 STAGE_SLOTS = 3
+# Round trip (pack, D2H, H2D, unpack): device slots per direction.  In a torch
+# process the HIP runtime carries each D2H copy as a blit kernel whose waves
+# hold the CUs until it drains, so packs and unpacks run only between those
+# copies.  With 3 slots every H2D copy waited for the unpack three chunks back,
+# and requests of 4-8 chunks ran at 22-37 GB/s per direction depending on how
+# the runtime mapped the streams onto hardware queues; with 4 slots they ran at
+# 37-41 in every mapping measured (MI355X, 32 layers, 64-128 MiB requests).
+# More slots gained nothing.
+ROUNDTRIP_SLOTS = 4
 MiB = 1 << 20
 
 
@@ -74,16 +83,18 @@ def chunk_layers(num_layers: int, layer_bytes: int) -> int:
 def roundtrip_chunk_layers(num_layers: int, layer_bytes: int) -> int:
     """Layers per chunk of the device->host->device round trip: the fewest
     layers whose chunks keep the pipeline out of the regime where many small
-    chunks stall it.  Measured on MI355X (32 layers, 64 MiB-1 GiB requests),
-    the round trip runs at 37-45 GB/s per direction with 16 MiB chunks when a
-    request has at most 8 of them, 32 MiB chunks up to 16 of them, or chunks
-    of 128 MiB and more at any count, but at 6-24 GB/s with 16 or more
-    chunks of 16 MiB or 32 chunks of 32 MiB."""
+    chunks stall it.  Measured on MI355X with ROUNDTRIP_SLOTS slots (32
+    layers, 64 MiB-1 GiB requests, four stream-to-queue mappings each), the
+    round trip runs at 38-46 GB/s per direction with chunks of 8 MiB and more
+    when a request has at most 8 of them, 32 MiB and more up to 16 of them, or
+    128 MiB and more at any count, but at 5-32 GB/s with 16 chunks of 4-8 MiB
+    or 32 chunks of up to 32 MiB.  Of the chunk sizes that qualify, the
+    smallest was the fastest or within 3% of it."""
     if layer_bytes <= 0:
         return max(1, num_layers)
     for k in range(1, num_layers + 1):
         chunk, count = k * layer_bytes, -(-num_layers // k)
-        if chunk >= 128 * MiB or (chunk >= 32 * MiB and count <= 16) or (chunk >= 16 * MiB and count <= 8):
+        if chunk >= 128 * MiB or (chunk >= 32 * MiB and count <= 16) or (chunk >= 8 * MiB and count <= 8):
             return k
     return max(1, num_layers)
 

@@ -348,8 +348,8 @@ class Promoter:
 
 class Stager:
     """Pinned-host staging pipeline (pace_kv_stager): device slot rings, side
-    streams for D2H copies, H2D copies and the round trip's unpacks, and the
-    events that order them.
+    streams for the round trip's packs and unpacks, D2H copies and H2D copies,
+    and the events that order them.
 
     Host tensors handed to a call are kept alive until the caller's stream has
     passed the point where the call's copies finish.  One host thread at a

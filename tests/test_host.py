@@ -141,9 +141,10 @@ def test_roundtrip_chunk_layers_avoid_many_small_chunks():
     MiB = 1 << 20
     # 32 layers of Llama-3-8B pages: requests of 512 .. 8192 tokens
     got = {tok: roundtrip_chunk_layers(32, tok // 16 * 64 * 1024) for tok in (512, 1024, 2048, 4096, 8192)}
-    assert got == {512: 8, 1024: 4, 2048: 4, 4096: 2, 8192: 2}
+    assert got == {512: 4, 1024: 4, 2048: 4, 4096: 2, 8192: 2}
     assert roundtrip_chunk_layers(32, 128 * MiB) == 1     # large chunks: any count
-    assert roundtrip_chunk_layers(32, 1 * MiB) == 16      # two 16 MiB chunks
+    assert roundtrip_chunk_layers(32, 1 * MiB) == 8       # four 8 MiB chunks
+    assert roundtrip_chunk_layers(32, 3 * MiB) == 4       # 12 MiB: 3 layers would make 11 chunks
     assert roundtrip_chunk_layers(32, MiB // 4) == 32     # 8 MiB in all: one chunk
     assert roundtrip_chunk_layers(80, 16 * MiB) == 5      # 80-layer cache: 16 chunks of 80 MiB
     for layers in (1, 7, 32, 80):
