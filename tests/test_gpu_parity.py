@@ -371,6 +371,44 @@ def test_roundtrips_on_two_streams_share_one_host_buffer(gpu):
         assert bad is None, f"call {i}: {bad}"
 
 
+@pytest.mark.parametrize("side", [False, True], ids=["null-stream", "side-stream"])
+def test_roundtrip_orders_against_the_callers_stream(gpu, side):
+    """The round trip's kernels run on a stream of the stager's own; the
+    caller's stream orders them all the same.  With no synchronisation
+    anywhere: the caller's stream spins (~20 ms), then writes new contents
+    into the source pool, then calls the round trip, then snapshots the
+    destination.  The snapshot holds the new contents at every moved page
+    (the packs waited for the write; the snapshot waited for the unpacks)."""
+    L, pages, shape = 6, 64, (2, 16, 2, 64)
+    page_bytes = int(np.prod(shape)) * 2
+    src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 700)
+    new = rand_pool(L, pages, shape, torch.bfloat16, gpu, 701)
+    dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 702)
+    before = [d.clone() for d in dst]
+    rng = np.random.default_rng(700)
+    n = 48
+    s_ids = rng.permutation(pages)[:n].tolist()
+    d_ids = rng.permutation(pages)[:n].tolist()
+    host = torch.empty(L * n * page_bytes, dtype=torch.uint8, pin_memory=True)
+    stream = torch.cuda.Stream(gpu) if side else torch.cuda.current_stream(gpu)
+    with ops.Stager(2 * n * page_bytes, 3) as st:
+        # the first call creates the host-ring events outside the timed order
+        st.roundtrip(src, s_ids, dst, d_ids, host, 2)
+        for d, b in zip(dst, before):
+            d.copy_(b)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(50_000_000)
+            for s, w in zip(src, new):
+                s.copy_(w)
+            st.roundtrip(src, s_ids, dst, d_ids, host, 2)
+            snap = [d.clone() for d in dst]
+        torch.cuda.synchronize()
+    bad = workloads.migration_mismatch(new, snap, torch.tensor(s_ids, device=gpu),
+                                       torch.tensor(d_ids, device=gpu), before)
+    assert bad is None, bad
+
+
 @pytest.mark.parametrize("seed", range(16))
 def test_random_staging_matches_torch(gpu, seed):
     """Seeded random pinned-host legs through one stager: layer counts on both
