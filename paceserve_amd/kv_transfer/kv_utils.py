@@ -82,14 +82,16 @@ def chunk_layers(num_layers: int, layer_bytes: int) -> int:
 
 def roundtrip_chunk_layers(num_layers: int, layer_bytes: int) -> int:
     """Layers per chunk of the device->host->device round trip: the fewest
-    layers whose chunks keep the pipeline out of the regime where many small
-    chunks stall it.  Measured on MI355X with ROUNDTRIP_SLOTS slots (32
-    layers, 64 MiB-1 GiB requests, four stream-to-queue mappings each), the
-    round trip runs at 38-46 GB/s per direction with chunks of 8 MiB and more
-    when a request has at most 8 of them, 32 MiB and more up to 16 of them, or
-    128 MiB and more at any count, but at 5-32 GB/s with 16 chunks of 4-8 MiB
-    or 32 chunks of up to 32 MiB.  Of the chunk sizes that qualify, the
-    smallest was the fastest or within 3% of it."""
+    layers giving chunks of 8 MiB and more when a request has at most 8 of
+    them, 32 MiB and more up to 16 of them, or 128 MiB and more at any count,
+    which keeps the pipeline out of the regime where many small chunks stall
+    it.  Measured on MI355X with ROUNDTRIP_SLOTS slots (32 layers, 64 KiB
+    pages, four stream-to-queue mappings each): for requests of 1536, 2048,
+    4096 and 8192 tokens the chosen chunks ran at 42-46 GB/s per direction
+    (median), within 3 GB/s of the best chunk size; 16 chunks of 4-8 MiB or
+    32 chunks of up to 32 MiB ran at 5-37.  Requests of 128 MiB and less ran
+    at 20-41 GB/s with any chunk size, depending on which hardware queues the
+    runtime gave the stager's streams."""
     if layer_bytes <= 0:
         return max(1, num_layers)
     for k in range(1, num_layers + 1):
