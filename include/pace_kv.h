@@ -234,8 +234,11 @@ int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers,
 /*
  * Full host round trip in one pipeline: pack(c) -> D2H(c) -> H2D(c) ->
  * unpack(c) per layer chunk, with pack(c+1), D2H(c), H2D(c-1) and the
- * unpacks of earlier chunks in flight together.  Packs, D2H copies and H2D
- * copies plus unpacks run on three streams of the stager's own: the packs
+ * unpacks of earlier chunks in flight together.  The D2H copies are a copy
+ * kernel of 16 waves when host_buf is pinned host memory the device can
+ * address (hipHostMalloc, torch's pin_memory), else hipMemcpyAsync; the H2D
+ * copies are hipMemcpyAsync.  Packs and unpacks, D2H copies and H2D copies run
+ * on three streams of the stager's own: the packs
  * start after the work enqueued on `stream` before the call, and `stream`
  * waits for everything the call enqueued, so `stream`'s later work comes
  * after the last unpack (also when the call fails part-way).  The copies

@@ -409,6 +409,60 @@ def test_roundtrip_orders_against_the_callers_stream(gpu, side):
     assert bad is None, bad
 
 
+def _hip_host_alloc(nbytes):
+    """hipHostMalloc of exactly nbytes, as (uint8 CPU tensor over it, free):
+    the caller synchronises and drops every view before calling free()."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    ptr = ctypes.c_void_p()
+    assert hip.hipHostMalloc(ctypes.byref(ptr), ctypes.c_size_t(nbytes), ctypes.c_uint(0)) == 0
+    arr = np.ctypeslib.as_array((ctypes.c_uint8 * nbytes).from_address(ptr.value))
+    return torch.from_numpy(arr), lambda: hip.hipHostFree(ptr)
+
+
+@pytest.mark.parametrize("kind", ["pageable", "pinned-at-offset", "pinned-to-the-end"])
+def test_roundtrip_host_buffer_kinds(gpu, kind):
+    """The round trip copies device to host with a kernel when the host
+    buffer is pinned memory the device addresses, and with hipMemcpyAsync
+    otherwise.  A pageable buffer, a pinned view starting 4 KiB into its
+    allocation, and a pinned view ending exactly at its allocation's end all
+    give the exact destination, two calls in a row; the second call's chunks
+    (656 KiB) are not a multiple of the kernel's 256 KiB pass, so its
+    remainder loop runs."""
+    L, pages, shape = 6, 64, (2, 16, 2, 64)
+    page_bytes = int(np.prod(shape)) * 2
+    src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 800)
+    rng = np.random.default_rng(800)
+    with ops.Stager(4 * 48 * page_bytes, 4) as st:
+        for rep in range(2):
+            n = 48 - rep * 7
+            need = L * n * page_bytes
+            free = None
+            if kind == "pageable":
+                host = torch.empty(need, dtype=torch.uint8)
+            elif kind == "pinned-at-offset":
+                host = torch.empty(need + 4096, dtype=torch.uint8, pin_memory=True)[4096:]
+            else:
+                # torch's host allocator rounds a block up; hipHostMalloc gives the exact size
+                base, free = _hip_host_alloc(need + 16)
+                host = base[16:]
+            s_ids = rng.permutation(pages)[:n].tolist()
+            d_ids = rng.permutation(pages)[:n].tolist()
+            dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 801 + rep)
+            before = [d.clone() for d in dst]
+            try:
+                st.roundtrip(src, s_ids, dst, d_ids, host, 2)
+            finally:
+                torch.cuda.synchronize()
+                if free is not None:
+                    st._inflight.clear()
+                    del host, base
+                    free()
+            bad = workloads.migration_mismatch(src, dst, torch.tensor(s_ids, device=gpu),
+                                               torch.tensor(d_ids, device=gpu), before)
+            assert bad is None, f"{kind} rep {rep}: {bad}"
+
+
 @pytest.mark.parametrize("seed", range(16))
 def test_random_staging_matches_torch(gpu, seed):
     """Seeded random pinned-host legs through one stager: layer counts on both
