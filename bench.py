@@ -1238,9 +1238,10 @@ def summarize_promote(trace_csv: str, bench_json: str, command: str) -> str:
 
 def summarize_copies(copy_csv: str, kernel_csv: str, bench_json: str, command: str) -> str:
     """Markdown summary of the pinned-host round trip from a rocprofv3
-    --memory-copy-trace (DMA-engine copies) and --kernel-trace (the runtime
-    runs some device-to-host copies as __amd_rocclr_copyBuffer blit kernels):
-    per-direction busy time and how long both directions ran at once."""
+    --memory-copy-trace (DMA-engine copies) and --kernel-trace (the round
+    trip's copy_to_host_kernel; hipMemcpyAsync device-to-host copies that the
+    runtime ran as __amd_rocclr_copyBuffer blit kernels): per-direction busy
+    time and how long both directions ran at once."""
     bench = _json(bench_json)
     st = bench.get("staging") or {}
     chunk = int(st.get("chunk_bytes", 0))
@@ -1253,7 +1254,9 @@ def summarize_copies(copy_csv: str, kernel_csv: str, bench_json: str, command: s
     for r in _rows(kernel_csv):
         s0, e0 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
         if "copyBuffer" in r["Kernel_Name"] and e0 - s0 > min_ns:
-            spans["D2H"].append((s0, e0, "blit kernel"))
+            spans["D2H"].append((s0, e0, "runtime blit kernel"))
+        elif "copy_to_host_kernel" in r["Kernel_Name"]:
+            spans["D2H"].append((s0, e0, "copy_to_host_kernel"))
     k = int(st.get("chunks", 0))
     # The last round trip: its k host-to-device copies are the run's last
     # ones; its device-to-host copies are the last k that end before them
