@@ -306,9 +306,11 @@ int unpack_chunk(pace_kv_stager* s, const ChunkPlan& p, int c, void* const* dst_
                         p.n_pages, p.page_bytes, err, stream);
 }
 
-// Makes `caller` wait for everything enqueued on the stager's work stream so
-// far: now() on the success path (reporting a failure), the destructor on an
-// early error return (best effort: the call is failing already).
+// Makes `caller` wait for everything a round trip enqueued: now() on the
+// success path (reporting a failure), where the last unpack on the work
+// stream already follows every copy; the destructor on an early error return
+// (best effort: the call is failing already), where copies may still be in
+// flight on the copy streams, so the work stream first waits for those too.
 struct WorkJoin {
   pace_kv_stager* s;
   hipStream_t caller;
@@ -320,8 +322,10 @@ struct WorkJoin {
     return PACE_KV_OK;
   }
   ~WorkJoin() {
-    if (!joined && hipEventRecord(s->work_done, s->work) == hipSuccess)
-      (void)hipStreamWaitEvent(caller, s->work_done, 0);
+    if (joined) return;
+    if (hipEventRecord(s->d2h_done, s->d2h) == hipSuccess) (void)hipStreamWaitEvent(s->work, s->d2h_done, 0);
+    if (hipEventRecord(s->h2d_done, s->h2d) == hipSuccess) (void)hipStreamWaitEvent(s->work, s->h2d_done, 0);
+    if (hipEventRecord(s->work_done, s->work) == hipSuccess) (void)hipStreamWaitEvent(caller, s->work_done, 0);
   }
 };
 

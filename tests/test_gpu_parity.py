@@ -1,6 +1,7 @@
 """Parity of the HIP path (libpace_kv.so through its C ABI) with the oracle,
 the golden fixtures and torch's own device gather/scatter.  Bit-exact: the
 path copies bytes, so every comparison is on raw integer words."""
+import ctypes
 from pathlib import Path
 
 import numpy as np
@@ -407,6 +408,47 @@ def test_roundtrip_orders_against_the_callers_stream(gpu, side):
     bad = workloads.migration_mismatch(new, snap, torch.tensor(s_ids, device=gpu),
                                        torch.tensor(d_ids, device=gpu), before)
     assert bad is None, bad
+
+
+def test_roundtrip_failing_part_way_leaves_the_stager_usable(gpu):
+    """A round trip whose destination table has a NULL pointer for the last
+    layer fails when it reaches that layer's chunk, on the host, after the
+    earlier chunks were packed, copied and unpacked (the NULL pointer never
+    reaches a kernel).  The call returns PACE_KV_EINVAL naming the layer, the
+    earlier chunks' destination layers are exact, the later ones untouched,
+    and the same stager then runs a full round trip exactly."""
+    L, pages, shape, n, k = 6, 64, (2, 16, 2, 64), 40, 2
+    page_bytes = int(np.prod(shape)) * 2
+    src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 900)
+    dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 901)
+    before = [d.clone() for d in dst]
+    rng = np.random.default_rng(900)
+    s_ids = rng.permutation(pages)[:n].tolist()
+    d_ids = rng.permutation(pages)[:n].tolist()
+    s_dev = torch.tensor(s_ids, dtype=torch.int32, device=gpu)
+    d_dev = torch.tensor(d_ids, dtype=torch.int32, device=gpu)
+    host = torch.empty(L * n * page_bytes, dtype=torch.uint8, pin_memory=True)
+    sp = ops.PagedPool(src)
+    table = _native.pointer_array([d.data_ptr() for d in dst[:-1]] + [None])
+    lib = _native.load()
+    with ops.Stager(k * n * page_bytes, 4) as st:
+        rc = lib.pace_kv_roundtrip(st._handle, sp.table(), pages, s_dev.data_ptr(), ctypes.addressof(table),
+                                   pages, d_dev.data_ptr(), L, n, page_bytes, k, host.data_ptr(),
+                                   host.numel(), None, ops._stream_handle(gpu))
+        torch.cuda.synchronize()
+        assert rc == _native.PACE_KV_EINVAL
+        assert "layer 1 pointer is NULL" in lib.pace_kv_last_error().decode()   # layer 1 of the last chunk
+        want = [words(b).clone() for b in before]
+        for l in range(L - k):
+            want[l][d_dev.long()] = words(src[l])[s_dev.long()]
+        for l in range(L):
+            assert torch.equal(words(dst[l]), want[l]), f"layer {l} after the failed call"
+        dst2 = rand_pool(L, pages, shape, torch.bfloat16, gpu, 902)
+        before2 = [d.clone() for d in dst2]
+        st.roundtrip(src, s_ids, dst2, d_ids, host, k)
+        torch.cuda.synchronize()
+        bad = workloads.migration_mismatch(src, dst2, s_dev, d_dev, before2)
+        assert bad is None, bad
 
 
 def _hip_host_alloc(nbytes):
