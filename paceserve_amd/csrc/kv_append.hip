@@ -54,6 +54,7 @@ struct AppendParams {
   uint32_t chunks_per_row;   // ceil(row_vecs / (V * 64))
   uint32_t total_items;      // nnz * 2 * chunks_per_row
   uint32_t row_vecs;         // row_bytes / 16
+  uint32_t guess_own_request;  // fused form, nnz <= batch_size: try request i for token i first
 };
 
 // A store of more than 64 bits reads its data registers after it issues; the
@@ -86,24 +87,48 @@ __device__ __forceinline__ int32_t request_of(const AppendParams& p, int32_t i) 
 // Page and slot of token i, or false when any index is out of range.
 template <bool FUSED>
 __device__ __forceinline__ bool locate(const AppendParams& p, uint32_t i, uint32_t* page, uint32_t* slot) {
-  int32_t b;
   int32_t pos;
+  int64_t first, last;
   if (FUSED) {
-    b = request_of(p, static_cast<int32_t>(i));
-    if (b < 0) return false;
-    const int32_t a0 = p.append_indptr[b], a1 = p.append_indptr[b + 1];
-    if (static_cast<int32_t>(i) >= a1) return false;
-    const int32_t pages = p.kv_indptr[b + 1] - p.kv_indptr[b];
-    const int32_t seq_len = (pages > 1 ? pages - 1 : 0) * static_cast<int32_t>(p.page_size) + p.kv_last_page_len[b];
-    pos = seq_len - (a1 - a0) + (static_cast<int32_t>(i) - a0);
+    const int32_t t = static_cast<int32_t>(i);
+    int32_t a0 = 0, a1 = 0, k0 = 0, k1 = 0, len = 0;
+    bool found = false;
+    if (p.guess_own_request && i < p.batch_size) {
+      // A decode batch (no more tokens than requests) usually appends one
+      // token per request: guess that token i is request i's and load every
+      // index that places it in one round.  The guess holds exactly when
+      // append_indptr[i] <= i < append_indptr[i+1], which is when the
+      // search below finds request i.
+      a0 = p.append_indptr[i];
+      a1 = p.append_indptr[i + 1];
+      k0 = p.kv_indptr[i];
+      k1 = p.kv_indptr[i + 1];
+      len = p.kv_last_page_len[i];
+      found = a0 <= t && t < a1;
+    }
+    if (!found) {
+      const int32_t b = request_of(p, t);
+      if (b < 0) return false;
+      a0 = p.append_indptr[b];
+      a1 = p.append_indptr[b + 1];
+      if (t >= a1) return false;
+      k0 = p.kv_indptr[b];
+      k1 = p.kv_indptr[b + 1];
+      len = p.kv_last_page_len[b];
+    }
+    const int32_t pages = k1 - k0;
+    const int32_t seq_len = (pages > 1 ? pages - 1 : 0) * static_cast<int32_t>(p.page_size) + len;
+    pos = seq_len - (a1 - a0) + (t - a0);
+    first = k0;
+    last = k1;
   } else {
-    b = p.batch_indices[i];
+    const int32_t b = p.batch_indices[i];
     pos = p.positions[i];
     if (b < 0 || static_cast<uint32_t>(b) >= p.batch_size) return false;
+    first = p.kv_indptr[b];
+    last = p.kv_indptr[b + 1];
   }
   if (pos < 0) return false;
-  const int64_t first = p.kv_indptr[b];
-  const int64_t last = p.kv_indptr[b + 1];
   const int64_t it = first + pos / static_cast<int32_t>(p.page_size);
   if (first < 0 || it >= last || it >= p.num_indices) return false;
   *page = static_cast<uint32_t>(p.kv_indices[it]);
@@ -238,6 +263,7 @@ int launch_append(AppendParams& p, int64_t nnz, int batch_size, int64_t num_page
   p.chunks_per_row = static_cast<uint32_t>(chunks);
   p.total_items = static_cast<uint32_t>(nnz * 2 * chunks);
   p.row_vecs = static_cast<uint32_t>(row_vecs);
+  p.guess_own_request = fused && nnz <= batch_size ? 1u : 0u;
   const bool guard = row_vecs % chunk_vecs != 0;
   const void* fn = fused ? pick_kernel<true>(v, guard, chunks > 1) : pick_kernel<false>(v, guard, chunks > 1);
   void* args[] = {&p};

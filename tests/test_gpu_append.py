@@ -246,3 +246,76 @@ def test_random_appends_match_numpy(gpu, seed):
     np.testing.assert_array_equal(words(two).cpu().numpy(), want)
     np.testing.assert_array_equal(words(fused).cpu().numpy(), want)
     assert int(err.item()) == 0
+
+
+@pytest.mark.parametrize("pattern", ["one-each", "uneven", "sparse"])
+@pytest.mark.parametrize("R", [7, 300])
+def test_decode_shaped_batches_match_numpy(gpu, pattern, R):
+    """Batches with no more tokens than requests, where the fused form first
+    tries request i for token i: one token per request (every guess right),
+    as many tokens as requests but spread 0/1/2 (some guesses wrong), and
+    fewer tokens than requests; 7 and 300 requests (the fallback search then
+    takes two rounds).  Both forms place every row where numpy does and leave
+    every other slot unchanged."""
+    rng = np.random.default_rng({"one-each": 1, "uneven": 2, "sparse": 3}[pattern] * 1000 + R)
+    P, H, D, dtype = 16, 8, 128, torch.bfloat16
+    if pattern == "one-each":
+        app = np.ones(R, dtype=np.int64)
+    elif pattern == "uneven":
+        app = rng.permutation(np.resize([0, 1, 2], R))       # sums to about R
+        app[-1] += R - int(app.sum())                         # exactly R tokens
+        assert app.min() >= 0
+    else:
+        app = (rng.random(R) < 0.6).astype(np.int64)          # 0 or 1, fewer tokens than requests
+    prior = rng.integers(0, 70, R)
+    total = prior + app
+    pages = -(-total // P)
+    NP = int(pages.sum()) + 3
+    kv_indptr = np.concatenate([[0], np.cumsum(pages)])
+    kv_indices = rng.permutation(NP)[: kv_indptr[-1]]
+    last = np.where(total == 0, 0, np.where(total % P == 0, P, total % P))
+    append_indptr = np.concatenate([[0], np.cumsum(app)])
+    nnz = int(append_indptr[-1])
+    assert nnz <= R
+    print(f"decode-shaped append {pattern} R={R} nnz={nnz}", flush=True)
+    raw = lambda shape: torch.empty(shape, dtype=torch.int8, device=gpu).copy_(
+        torch.from_numpy(rng.integers(-2 ** 7, 2 ** 7, shape).astype(np.int8)))
+    k = raw((nnz, H, D * 2)).view(dtype).view(nnz, H, D)
+    v = raw((nnz, H, D * 2)).view(dtype).view(nnz, H, D)
+    cache = raw((NP, 2, P, H, D * 2)).view(dtype).view(NP, 2, P, H, D)
+    want = words(cache).cpu().numpy().copy()
+    b = np.repeat(np.arange(R), app)
+    pos = total[b] - app[b] + (np.arange(nnz) - append_indptr[b])
+    page = kv_indices[kv_indptr[b] + pos // P]
+    want[page, 0, pos % P] = words(k).cpu().numpy()
+    want[page, 1, pos % P] = words(v).cpu().numpy()
+    two = cache.clone()
+    seq = ap.get_seq_lens(i32(kv_indptr, gpu), i32(last, gpu), P)
+    bi, ps = ap.get_batch_indices_positions(i32(append_indptr, gpu), seq, nnz)
+    ap.append_paged_kv_cache(k, v, bi, ps, two, i32(kv_indices, gpu), i32(kv_indptr, gpu), i32(last, gpu))
+    fused = cache.clone()
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ap.append_paged_kv_cache_indptr(k, v, i32(append_indptr, gpu), fused, i32(kv_indices, gpu),
+                                    i32(kv_indptr, gpu), i32(last, gpu), err=err)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(words(two).cpu().numpy(), want)
+    np.testing.assert_array_equal(words(fused).cpu().numpy(), want)
+    assert int(err.item()) == 0
+
+
+def test_fused_decode_batch_skips_and_counts_tokens_out_of_range(gpu):
+    """The same rules when the fused form first tries request i for token i
+    (5 tokens, 5 requests): request 1's last-page length puts its token
+    before position 0, request 2's page id is past the cache, request 4
+    appends nothing so token 4 is beyond the last request's offsets; those
+    three are skipped and counted, requests 0 and 3 land."""
+    cache = torch.zeros(4, 2, 4, 1, 64, dtype=torch.float16, device=gpu)
+    k = torch.ones(5, 1, 64, dtype=torch.float16, device=gpu)
+    ai = i32([0, 1, 2, 3, 4, 4], gpu)
+    kv_indptr, kv_indices, last = i32([0, 1, 2, 3, 4, 5], gpu), i32([3, 1, 9, 2, 0], gpu), i32([1, 0, 1, 3, 1], gpu)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    ap.append_paged_kv_cache_indptr(k, k, ai, cache, kv_indices, kv_indptr, last, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 3
+    assert (cache[3, :, 0] == 1).all() and (cache[2, :, 2] == 1).all()
+    assert int((cache != 0).sum()) == 2 * 2 * 64
