@@ -120,18 +120,20 @@ struct pace_kv_stager {
   int num_slots = 0;
   char* out_ring = nullptr;  // num_slots device slots written by pack, read by D2H
   char* in_ring = nullptr;   // num_slots device slots written by H2D, read by unpack
-  hipStream_t work = nullptr;
+  hipStream_t work = nullptr;  // the round trip's packs and unpacks
   hipStream_t d2h = nullptr;
   hipStream_t h2d = nullptr;
-  hipEvent_t work_start = nullptr;
-  hipEvent_t work_done = nullptr;
+  hipEvent_t work_start = nullptr;  // the caller's stream at the start of a round trip
+  hipEvent_t work_done = nullptr;   // everything a round trip enqueued
   hipEvent_t start = nullptr;
   hipEvent_t d2h_done = nullptr;
   hipEvent_t h2d_done = nullptr;  // the last round trip's last H2D copy
-  std::vector<hipEvent_t> packed;    // out slot s filled (caller stream)
+  // The kernel stream below is the work stream in a round trip and the
+  // caller's stream in the one-way legs.
+  std::vector<hipEvent_t> packed;    // out slot s filled (kernel stream)
   std::vector<hipEvent_t> out_free;  // out slot s drained by D2H (D2H stream)
   std::vector<hipEvent_t> in_ready;  // in slot s filled by H2D (H2D stream)
-  std::vector<hipEvent_t> in_free;   // in slot s drained by unpack (caller stream)
+  std::vector<hipEvent_t> in_free;   // in slot s drained by unpack (kernel stream)
   std::vector<hipEvent_t> host_full;  // host region r written by D2H
   std::vector<hipEvent_t> host_free;  // host region r read by H2D
 };
