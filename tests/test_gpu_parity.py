@@ -410,6 +410,44 @@ def test_roundtrip_orders_against_the_callers_stream(gpu, side):
     assert bad is None, bad
 
 
+def test_mixed_stager_calls_on_two_streams_without_synchronisation(gpu):
+    """One stager's slots and events order every kind of call against the
+    others: a round trip on stream A, a pack to host on stream B, an unpack
+    from host on stream A and a round trip on stream B, enqueued back to back
+    with no synchronisation (the four calls move independent data), all end
+    exact."""
+    L, pages, shape, n, k = 6, 48, (2, 16, 2, 64), 40, 2
+    page_bytes = int(np.prod(shape)) * 2
+    rng = np.random.default_rng(950)
+    srcs = [rand_pool(L, pages, shape, torch.bfloat16, gpu, 950 + i) for i in range(4)]
+    dsts = [rand_pool(L, pages, shape, torch.bfloat16, gpu, 960 + i) for i in range(4)]
+    befores = [[d.clone() for d in dst] for dst in dsts]
+    s_ids = [rng.permutation(pages)[:n].tolist() for _ in range(4)]
+    d_ids = [rng.permutation(pages)[:n].tolist() for _ in range(4)]
+    ring = [torch.empty(3 * k * n * page_bytes, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+    host_out = torch.empty((L, n) + shape, dtype=torch.bfloat16, pin_memory=True)
+    # the unpack's input: call 2's source pages, gathered by torch
+    host_in = torch.stack([s[torch.tensor(s_ids[2], device=gpu)] for s in srcs[2]]).cpu().pin_memory()
+    streams = [torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)]
+    torch.cuda.synchronize()
+    with ops.Stager(k * n * page_bytes, 4) as st:
+        with torch.cuda.stream(streams[0]):
+            st.roundtrip(srcs[0], s_ids[0], dsts[0], d_ids[0], ring[0], k)
+        with torch.cuda.stream(streams[1]):
+            st.pack_to_host(srcs[1], s_ids[1], host_out, k)
+        with torch.cuda.stream(streams[0]):
+            st.unpack_from_host(host_in, dsts[2], d_ids[2], k)
+        with torch.cuda.stream(streams[1]):
+            st.roundtrip(srcs[3], s_ids[3], dsts[3], d_ids[3], ring[1], k)
+        torch.cuda.synchronize()
+    for i in (0, 2, 3):
+        bad = workloads.migration_mismatch(srcs[i], dsts[i], torch.tensor(s_ids[i], device=gpu),
+                                           torch.tensor(d_ids[i], device=gpu), befores[i])
+        assert bad is None, f"call {i}: {bad}"
+    want = torch.stack([s[torch.tensor(s_ids[1], device=gpu)] for s in srcs[1]]).cpu()
+    assert torch.equal(words(host_out), words(want)), "call 1: pack to host"
+
+
 def test_roundtrip_failing_part_way_leaves_the_stager_usable(gpu):
     """A round trip whose destination table has a NULL pointer for the last
     layer fails when it reaches that layer's chunk, on the host, after the
