@@ -736,9 +736,19 @@ def link_settle(dev, target_gbs: float = 45.0, max_wait_s: float = 30.0, streak:
     return {"d2h_gbs": round(rate, 1), "waited_s": round(waited, 2), "settled": good >= streak}
 
 
-def run_staging(w, dev, src, dst, s_ids, d_ids, reps: int = 3):
+def staging_chunk_bytes(w) -> int:
+    """Bytes of one layer chunk of a workload's pinned-host legs."""
+    from paceserve_amd.kv_transfer import kv_utils
+
+    layer_bytes = w.n_pages * w.shape.page_bytes
+    k = w.layers_per_chunk or kv_utils.roundtrip_chunk_layers(w.shape.num_layers, layer_bytes)
+    return k * layer_bytes
+
+
+def run_staging(w, dev, src, dst, s_ids, d_ids, stager, reps: int = 3):
     """Pinned-host legs: pack_to_host, unpack_from_host and the overlapped
-    round trip, in GB/s per direction against the PCIe Gen5 x16 peak."""
+    round trip, in GB/s per direction against the PCIe Gen5 x16 peak, through
+    `stager` (one for the whole process, as a serving worker keeps its own)."""
     import torch
 
     from paceserve_amd.kv_transfer import kv_utils, ops
@@ -748,6 +758,8 @@ def run_staging(w, dev, src, dst, s_ids, d_ids, reps: int = 3):
     k = w.layers_per_chunk or kv_utils.roundtrip_chunk_layers(L, layer_bytes)
     chunk = k * layer_bytes
     chunks = -(-L // k)
+    if stager.slot_bytes < chunk:
+        raise ValueError(f"stager slots of {stager.slot_bytes} B cannot hold {w.name}'s {chunk} B chunks")
     # host ring of up to 4 chunk regions (a full copy for short payloads)
     host_bytes = min(w.payload_bytes, 4 * chunk)
     host = torch.empty(host_bytes, dtype=torch.uint8, pin_memory=True)
@@ -768,15 +780,16 @@ def run_staging(w, dev, src, dst, s_ids, d_ids, reps: int = 3):
 
     out = {"layers_per_chunk": k, "chunks": chunks, "chunk_bytes": chunk, "host_ring_bytes": host_bytes,
            "pcie_peak_gbs_per_direction": 64.0}
-    with ops.Stager(-(-chunk // 256) * 256, kv_utils.ROUNDTRIP_SLOTS, dev) as st:
-        t_rt = timed(lambda: st.roundtrip(src, s_ids, dst, d_ids, host, k))
-        out["roundtrip_ms"] = round(t_rt * 1e3, 3)
-        out["roundtrip_gbs_per_direction"] = round(w.payload_bytes / t_rt / 1e9, 2)
-        if full is not None:
-            t_d2h = timed(lambda: st.pack_to_host(src, s_ids, full, k))
-            t_h2d = timed(lambda: st.unpack_from_host(full, dst, d_ids, k))
-            out["pack_to_host_gbs"] = round(w.payload_bytes / t_d2h / 1e9, 2)
-            out["unpack_from_host_gbs"] = round(w.payload_bytes / t_h2d / 1e9, 2)
+    st = stager
+    t_rt = timed(lambda: st.roundtrip(src, s_ids, dst, d_ids, host, k))
+    out["roundtrip_ms"] = round(t_rt * 1e3, 3)
+    out["roundtrip_gbs_per_direction"] = round(w.payload_bytes / t_rt / 1e9, 2)
+    if full is not None:
+        t_d2h = timed(lambda: st.pack_to_host(src, s_ids, full, k))
+        t_h2d = timed(lambda: st.unpack_from_host(full, dst, d_ids, k))
+        out["pack_to_host_gbs"] = round(w.payload_bytes / t_d2h / 1e9, 2)
+        out["unpack_from_host_gbs"] = round(w.payload_bytes / t_h2d / 1e9, 2)
+    torch.cuda.synchronize()
     log(f"staging: round trip {out['roundtrip_ms']} ms = {out['roundtrip_gbs_per_direction']} GB/s per direction")
     return out
 
@@ -810,7 +823,7 @@ CPU_CONFIG_SECONDS = 3.0
 CPU_CONFIG_LAYERS = 4
 
 
-def run_staging_leg(args, name: str, dev) -> dict:
+def run_staging_leg(args, name: str, dev, stager) -> dict:
     """The pinned-host legs of a workload (run_staging) on its own pools,
     then the exact check of both pools (the round trip writes the same
     destination pages as the device path)."""
@@ -819,7 +832,7 @@ def run_staging_leg(args, name: str, dev) -> dict:
     w = workloads.get(name)
     log(f"staging {w.name}: {w.description}")
     src, dst, plan, s_ids, d_ids = device_setup(w, dev)
-    st = run_staging(w, dev, src, dst, s_ids, d_ids)
+    st = run_staging(w, dev, src, dst, s_ids, d_ids, stager)
     st["workload"] = w.name
     if args.verify:
         st["verified"] = verify(w, src, dst, s_ids, d_ids, dev)
@@ -1475,6 +1488,17 @@ def main():
                               if n != w.name and workloads.get(n).staging in ("pinned", "both")]
     promote = None
     early_staging = {}
+    # One stager for every staging leg, created before them and kept to the
+    # end of the process, as a serving worker creates its own once: the
+    # round trip measured after every other leg then runs on the same
+    # stager as the first one.  A stager created late in a process was
+    # measured to run small requests slower (29-38 against 37 GB/s).
+    stager = None
+    if staging_names:
+        from paceserve_amd.kv_transfer import kv_utils, ops
+
+        slot = max(staging_chunk_bytes(workloads.get(n)) for n in staging_names)
+        stager = ops.Stager(-(-slot // 256) * 256, kv_utils.ROUNDTRIP_SLOTS, dev)
     if staging_names or not args.no_promote:
         settle = link_settle(dev)
         log(f"host link settled after {settle['waited_s']} s at {settle['d2h_gbs']} GB/s D2H")
@@ -1482,7 +1506,7 @@ def main():
             promote = run_promote(dev, c_caller=not args.no_c_caller)
             promote["link_probe"] = settle
         for name in staging_names:
-            early_staging[name] = run_staging_leg(args, name, dev)
+            early_staging[name] = run_staging_leg(args, name, dev, stager)
             early_staging[name]["link_probe"] = settle
     if early_staging:
         # The staging pools go back to the driver, which scrubs them with the
@@ -1539,8 +1563,10 @@ def main():
         staging_warm = {}
         for name in early_staging:
             settle = link_settle(dev)
-            staging_warm[name] = run_staging_leg(args, name, dev)
+            staging_warm[name] = run_staging_leg(args, name, dev, stager)
             staging_warm[name]["link_probe"] = settle
+    if stager is not None:
+        stager.close()
 
     line = {
         "metric": METRIC,
