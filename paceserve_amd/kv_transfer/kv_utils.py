@@ -37,15 +37,12 @@ from . import ops
 # request into more chunks gains nothing.
 STAGE_CHUNK_BYTES = 64 << 20
 STAGE_SLOTS = 3
-# Round trip (pack, D2H, H2D, unpack): device slots per direction.  In a torch
-# process the HIP runtime carries each D2H copy as a blit kernel whose waves
-# hold the CUs until it drains, so packs and unpacks run only between those
-# copies.  With 3 slots every H2D copy waited for the unpack three chunks back,
-# and requests of 4-8 chunks ran at 22-37 GB/s per direction depending on how
-# the runtime mapped the streams onto hardware queues; with 4 slots they ran at
-# 37-41 in every mapping measured (MI355X, 32 layers, 64-128 MiB requests).
-# More slots gained nothing.
-ROUNDTRIP_SLOTS = 4
+# Round trip (pack, D2H, H2D, unpack): device slots per direction.  Measured on
+# MI355X on stagers created once and kept (none freed during the measurement),
+# 3 and 4 slots ran within 2% of each other at every request size from 256 to
+# 8192 tokens, with no size favouring either, so the round trip takes 3, the
+# less device memory.
+ROUNDTRIP_SLOTS = 3
 MiB = 1 << 20
 
 
@@ -85,13 +82,11 @@ def roundtrip_chunk_layers(num_layers: int, layer_bytes: int) -> int:
     layers giving chunks of 8 MiB and more when a request has at most 8 of
     them, 32 MiB and more up to 16 of them, or 128 MiB and more at any count,
     which keeps the pipeline out of the regime where many small chunks stall
-    it.  Measured on MI355X with ROUNDTRIP_SLOTS slots (32 layers, 64 KiB
-    pages, four stream-to-queue mappings each): for requests of 1536, 2048,
-    4096 and 8192 tokens the chosen chunks ran at 42-46 GB/s per direction
-    (median), within 3 GB/s of the best chunk size; 16 chunks of 4-8 MiB or
-    32 chunks of up to 32 MiB ran at 5-37.  Requests of 128 MiB and less ran
-    at 20-41 GB/s with any chunk size, depending on which hardware queues the
-    runtime gave the stager's streams."""
+    it (16 chunks of 4-8 MiB, or 32 chunks, ran at 5-37 GB/s per direction).
+    Measured on MI355X on stagers created once and kept (32 layers, 64 KiB
+    pages): for 256-1024-token requests the chosen 8-16 MiB chunks ran 2-5%
+    faster than chunks twice as large (32-41 GB/s), and for 2048-8192 tokens
+    the choice was the fastest measured or within 1.4% of it (42-46 GB/s)."""
     if layer_bytes <= 0:
         return max(1, num_layers)
     for k in range(1, num_layers + 1):

@@ -353,10 +353,10 @@ class Stager:
 
     Host tensors handed to a call are kept alive until the caller's stream has
     passed the point where the call's copies finish.  One host thread at a
-    time may drive a stager.  The default of 4 slots is the round trip's
-    (kv_utils.ROUNDTRIP_SLOTS); the one-way legs need 2-3."""
+    time may drive a stager.  Two slots are the minimum; three (the default,
+    kv_utils.ROUNDTRIP_SLOTS) measured as fast as four."""
 
-    def __init__(self, slot_bytes: int, num_slots: int = 4, device: Optional[torch.device] = None):
+    def __init__(self, slot_bytes: int, num_slots: int = 3, device: Optional[torch.device] = None):
         self.device = torch.device(device) if device is not None else torch.device(
             "cuda", torch.cuda.current_device())
         handle = ctypes.c_void_p()
