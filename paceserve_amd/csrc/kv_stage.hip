@@ -31,8 +31,9 @@
 // In a torch process the HIP runtime is the one torch ships.  It carried
 // hipMemcpyAsync D2H copies as blit kernels whose waves hold the CUs until
 // the copy drains, so that packs and unpacks ran only between those copies,
-// and switched some of them, by rules of its own, to a DMA engine that moved
-// them at a quarter of the link's rate.  The round trip therefore copies
+// and switched some of them, by rules of its own, to a DMA engine, where they
+// ran one after the other with the H2D copies (12.8 GB/s).  The round trip
+// therefore copies
 // device to host with a kernel of its own, sized to leave the CUs to the
 // packs and unpacks (copy_to_host_kernel).  Its packs and unpacks run on a
 // work stream of the stager's own, which keeps them off whatever else the
