@@ -33,9 +33,8 @@
 // the copy drains, so that packs and unpacks ran only between those copies,
 // and switched some of them, by rules of its own, to a DMA engine, where they
 // ran one after the other with the H2D copies (12.8 GB/s).  The round trip
-// therefore copies
-// device to host with a kernel of its own, sized to leave the CUs to the
-// packs and unpacks (copy_to_host_kernel).  Its packs and unpacks run on a
+// therefore copies device to host with a kernel of its own, sized to leave
+// the CUs to the packs and unpacks (copy_to_host_kernel).  Its packs and unpacks run on a
 // work stream of the stager's own, which keeps them off whatever else the
 // caller's stream carries; measured against the caller's stream on stagers
 // kept for the whole run, it was 2% and 6% faster for 2048- and 4096-token
