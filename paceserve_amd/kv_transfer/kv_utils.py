@@ -44,6 +44,19 @@ STAGE_SLOTS = 3
 # less device memory.
 ROUNDTRIP_SLOTS = 3
 MiB = 1 << 20
+STAGE_GROWTH_CAP = 256 * MiB
+
+
+def grown_slot_bytes(needed: int, current: int = 0) -> int:
+    """Slot bytes for a stager that must hold `needed` bytes per slot and
+    replaces one of `current` bytes (0: no stager yet), a multiple of 256.
+    Freeing a stager's device rings makes the driver scrub that memory with
+    the DMA engines the host-to-device copies use (round trips started
+    meanwhile measured up to 30% slower), so a stager that must grow at least
+    doubles, by at most STAGE_GROWTH_CAP beyond what is needed: a run of
+    growing requests replaces it a few times, not once per new size."""
+    grown = needed if current <= 0 else max(needed, min(2 * current, needed + STAGE_GROWTH_CAP))
+    return -(-grown // 256) * 256
 
 
 def normalize_page_ids(ids: Sequence[int], num_pages: int) -> List[int]:
@@ -135,12 +148,14 @@ class KVhelper:
 
     def _stager_for(self, pool: ops.PagedPool, slot_bytes: int) -> ops.Stager:
         st = self._stager
+        current = 0
         if st is not None and (st.slot_bytes < slot_bytes or st.device != pool.device):
+            current = st.slot_bytes if st.device == pool.device else 0
             torch.cuda.current_stream(st.device).synchronize()
             st.close()
             st = None
         if st is None:
-            st = ops.Stager(-(-slot_bytes // 256) * 256, STAGE_SLOTS, pool.device)
+            st = ops.Stager(grown_slot_bytes(slot_bytes, current), STAGE_SLOTS, pool.device)
             self._stager = st
         return st
 

@@ -215,14 +215,16 @@ class KVMigrator:
                 ops.pack(self.src, src_ids, buf[: le - lb], layer_begin=lb, layer_end=le)
                 ops.unpack(buf[: le - lb], self.dst, dst_ids, layer_begin=lb, layer_end=le)
         elif mode == "pinned":
-            from .kv_utils import ROUNDTRIP_SLOTS, roundtrip_chunk_layers
+            from .kv_utils import ROUNDTRIP_SLOTS, grown_slot_bytes, roundtrip_chunk_layers
             k = layers_per_chunk or roundtrip_chunk_layers(L, n * self.src.page_bytes)
             slot = k * n * self.src.page_bytes
             if self.stager is None or self.stager.slot_bytes < slot:
+                current = 0
                 if self.stager is not None:
+                    current = self.stager.slot_bytes
                     torch.cuda.current_stream(self.src.device).synchronize()
                     self.stager.close()
-                self.stager = ops.Stager(-(-slot // 256) * 256, ROUNDTRIP_SLOTS, self.src.device)
+                self.stager = ops.Stager(grown_slot_bytes(slot, current), ROUNDTRIP_SLOTS, self.src.device)
             if host_buf is None:
                 host_buf = torch.empty(L * n * self.src.page_bytes, dtype=torch.uint8, pin_memory=True)
             self.stager.roundtrip(self.src, src_ids, self.dst, dst_ids, host_buf, k)

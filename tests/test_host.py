@@ -8,7 +8,7 @@ from paceserve_amd.core.block_manager import BlockAllocator, BlockSpaceManager, 
 from paceserve_amd.core.kv_cache_obj import KVobj
 from paceserve_amd.core.sequence import Sequence
 from paceserve_amd.kv_transfer.kv_utils import (chunk_layers, dedup_keep_last, normalize_page_ids,
-                                                roundtrip_chunk_layers)
+                                                grown_slot_bytes, roundtrip_chunk_layers)
 from paceserve_amd.kv_transfer.migrate import flatten_tables, plan_batch
 from paceserve_amd.kv_transfer.worker import KVStatus, KVWorker, WorkerSequenceManager
 
@@ -135,6 +135,20 @@ def test_chunk_layers():
     assert chunk_layers(32, 3 * MiB) == 22       # the fewest layers reaching 64 MiB
     assert chunk_layers(32, 512 * MiB) == 1
     assert chunk_layers(1, 1) == 1 and chunk_layers(5, 0) == 5
+
+
+def test_grown_slot_bytes_at_least_double_within_the_cap():
+    MiB = 1 << 20
+    assert grown_slot_bytes(10 * MiB + 3) == 10 * MiB + 256          # first stager: what is needed
+    assert grown_slot_bytes(12 * MiB, 10 * MiB) == 20 * MiB          # growing: at least double
+    assert grown_slot_bytes(50 * MiB, 10 * MiB) == 50 * MiB          # more than double: what is needed
+    assert grown_slot_bytes(1024 * MiB, 900 * MiB) == 1280 * MiB     # doubling capped 256 MiB past the need
+    sizes, cur, replaced = [8 * MiB + i * MiB for i in range(200)], 0, 0
+    for need in sizes:                                               # a run of growing requests
+        if cur < need:
+            cur, replaced = grown_slot_bytes(need, cur), replaced + 1
+        assert cur >= need and cur % 256 == 0
+    assert replaced <= 6
 
 
 def test_roundtrip_chunk_layers_avoid_many_small_chunks():
