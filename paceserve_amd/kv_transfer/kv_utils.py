@@ -40,8 +40,8 @@ STAGE_SLOTS = 3
 # Round trip (pack, D2H, H2D, unpack): device slots per direction.  Measured on
 # MI355X on stagers created once and kept (none freed during the measurement),
 # 3 and 4 slots ran within 2% of each other at every request size from 256 to
-# 8192 tokens, with no size favouring either, so the round trip takes 3, the
-# less device memory.
+# 8192 tokens, with no size favouring either, so the round trip takes 3,
+# which holds less device memory.
 ROUNDTRIP_SLOTS = 3
 MiB = 1 << 20
 STAGE_GROWTH_CAP = 256 * MiB
