@@ -168,7 +168,8 @@ int pace_kv_stager_destroy(pace_kv_stager* stager);
  * layout [num_layers, n_pages, page_size-slice...] of PACK with
  * out_layer_stride = n_pages * page_bytes.  Pinned host memory gives
  * asynchronous DMA; pageable memory works but the runtime stages it.
- * When the call returns, `stream` is ordered after the last copy.
+ * When the call returns, `stream` is ordered after the last copy.  A call of
+ * one chunk (layers_per_chunk >= num_layers) packs and copies on `stream`.
  *
  * Replaces the gather + pageable device-to-host copy loop of
  * KVhelper.get_kv_cache (paceserve/kv_transfer/kv_utils.py:44-47).
@@ -183,7 +184,7 @@ int pace_kv_pack_to_host(pace_kv_stager* stager,
 /*
  * Unpack from host memory: the mirror of pace_kv_pack_to_host.  Chunk c is
  * copied host-to-device on the H2D side stream while chunk c-1 is unpacked on
- * `stream`.
+ * `stream`; a call of one chunk copies and unpacks on `stream`.
  *
  * Replaces the pageable host-to-device copy + scatter loop of
  * KVhelper.insert_kv_cache (paceserve/kv_transfer/kv_utils.py:49-52).
@@ -244,7 +245,8 @@ int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers,
  * after the last unpack (also when the call fails part-way).  The copies
  * overlap however the runtime maps these streams onto its hardware queues.
  * Calls on one stager run their packs and unpacks in call order, whichever
- * `stream` each names.
+ * `stream` each names.  A call of one chunk has nothing to overlap and runs
+ * its four stages on `stream`, after the stager's earlier calls.
  * host_buf holds host_bytes of host memory used as a ring of chunk-sized
  * regions (host_bytes >= one chunk; pass the full payload to keep a complete
  * host copy, as the reference's KVobj does).

@@ -40,6 +40,10 @@
 // kept for the whole run, it was 2% and 6% faster for 2048- and 4096-token
 // requests and within 2% either way for 256-1024 and 8192 tokens.
 //
+// A call whose layers fit one chunk has nothing to overlap, so all its stages
+// run on the caller's stream: each wait between streams adds latency, 30-36 us
+// per call on 2-8 MiB requests.
+//
 // Device slots are reused round-robin; before a slot is overwritten, the
 // stream that writes it waits for the event recorded after the last read of
 // that slot, so back-to-back calls on one stager are ordered correctly.
@@ -377,6 +381,7 @@ int pace_kv_stager_destroy(pace_kv_stager* s) {
   hipError_t e2 = hipStreamSynchronize(s->h2d);
   for (hipEvent_t e : s->in_free) (void)hipEventSynchronize(e);
   for (hipEvent_t e : s->packed) (void)hipEventSynchronize(e);
+  for (hipEvent_t e : s->out_free) (void)hipEventSynchronize(e);  // one-chunk copies on the caller's stream
   release(s);
   if (e1 != hipSuccess) return hip_status(e1, "stager_destroy (D2H stream)");
   return hip_status(e2, "stager_destroy (H2D stream)");
@@ -393,6 +398,17 @@ int pace_kv_pack_to_host(pace_kv_stager* s, const void* const* src_layers, int n
   if (host_out == nullptr) return fail(PACE_KV_EINVAL, "pack_to_host: host_out is NULL");
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   const int chunks = p.num_chunks();
+  if (chunks == 1) {
+    // One chunk leaves nothing to overlap: the pack and the copy run on
+    // `stream`, without the waits between streams (measured on MI355X: 30-36
+    // us less per call for 2-8 MiB requests, about 1% less at 128 MiB).
+    PACE_HIP(hipStreamWaitEvent(stream, s->out_free[0], 0), "wait out slot");
+    PACE_KV_TRY(pack_chunk(s, p, 0, src_layers, pool_pages, page_ids, err_count, stream));
+    PACE_HIP(hipMemcpyAsync(host_out, s->out_ring, p.count(0) * p.layer_bytes, hipMemcpyDeviceToHost, stream),
+             "D2H copy");
+    PACE_HIP(hipEventRecord(s->out_free[0], stream), "record out_free");
+    return PACE_KV_OK;
+  }
   // Step i enqueues pack(i + 1), then the copy of chunk i: the copy's
   // completion record, which holds back whatever follows it when the D2H
   // stream shares the caller's hardware queue, then only delays pack(i + 2).
@@ -430,10 +446,20 @@ int pace_kv_unpack_from_host(pace_kv_stager* s, const void* host_in, void* const
   if (num_layers == 0 || n_pages == 0) return PACE_KV_OK;
   if (host_in == nullptr) return fail(PACE_KV_EINVAL, "unpack_from_host: host_in is NULL");
   hipStream_t stream = static_cast<hipStream_t>(stream_);
+  const int chunks = p.num_chunks();
+  if (chunks == 1) {
+    // One chunk: the copy and the unpack run on `stream` (as in the pack).
+    PACE_HIP(hipStreamWaitEvent(stream, s->in_free[0], 0), "wait in slot");
+    PACE_HIP(hipMemcpyAsync(s->in_ring, host_in, p.count(0) * p.layer_bytes, hipMemcpyHostToDevice, stream),
+             "H2D copy");
+    // in_free follows the copy also when the unpack fails to launch.
+    const int rc = unpack_chunk(s, p, 0, dst_layers, pool_pages, page_ids, err_count, stream);
+    PACE_HIP(hipEventRecord(s->in_free[0], stream), "record in_free");
+    return rc;
+  }
   // The caller's earlier work (e.g. writes of host_in by a kernel) comes first.
   PACE_HIP(hipEventRecord(s->start, stream), "record start");
   PACE_HIP(hipStreamWaitEvent(s->h2d, s->start, 0), "wait start");
-  const int chunks = p.num_chunks();
   // Step i enqueues the copy of chunk i + 1, then unpack(i), whose wait for
   // chunk i's copy then holds back (on a shared hardware queue) only the copy
   // of chunk i + 2.  That copy refills the slot of chunk i + 2 - num_slots,
@@ -478,6 +504,31 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
   const int regions = regions64 < chunks ? static_cast<int>(regions64) : chunks;
   PACE_HIP(make_events(s->host_full, regions), "create host events");
   PACE_HIP(make_events(s->host_free, regions), "create host events");
+  char* host = static_cast<char*>(host_buf);
+  const bool host_kernel = device_addressable_host(host_buf, regions * chunk_bytes);
+  if (chunks == 1) {
+    // One chunk leaves nothing to overlap: its four stages run on the
+    // caller's stream, without the waits between streams.  They follow the
+    // packs and unpacks of earlier calls on this stager (work_done), the last
+    // reads of both slots and the previous call's last read of its host
+    // buffer, and leave the records a later call waits on.
+    hipStream_t caller = static_cast<hipStream_t>(stream_);
+    const int64_t bytes = p.count(0) * p.layer_bytes;
+    PACE_HIP(hipStreamWaitEvent(caller, s->work_done, 0), "wait earlier calls");
+    PACE_HIP(hipStreamWaitEvent(caller, s->out_free[0], 0), "wait out slot");
+    PACE_HIP(hipStreamWaitEvent(caller, s->h2d_done, 0), "wait previous round trip");
+    PACE_KV_TRY(pack_chunk(s, p, 0, src_layers, src_pool_pages, src_ids, err_count, caller));
+    PACE_HIP(copy_to_host(host, s->out_ring, bytes, host_kernel, caller), "D2H copy");
+    PACE_HIP(hipEventRecord(s->out_free[0], caller), "record out_free");
+    PACE_HIP(hipStreamWaitEvent(caller, s->in_free[0], 0), "wait in slot");
+    PACE_HIP(hipMemcpyAsync(s->in_ring, host, bytes, hipMemcpyHostToDevice, caller), "H2D copy");
+    PACE_HIP(hipEventRecord(s->h2d_done, caller), "record h2d_done");
+    // The records follow the H2D copy also when the unpack fails to launch.
+    const int rc = unpack_chunk(s, p, 0, dst_layers, dst_pool_pages, dst_ids, err_count, caller);
+    PACE_HIP(hipEventRecord(s->in_free[0], caller), "record in_free");
+    PACE_HIP(hipEventRecord(s->work_done, caller), "record work_done");
+    return rc;
+  }
   // Packs and unpacks run on the stager's work stream, created together with
   // its two copy streams (see the file comment); the work stream starts after
   // the caller's earlier work, and the caller's stream waits for everything
@@ -487,9 +538,7 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
   WorkJoin join{s, caller};
   PACE_HIP(hipEventRecord(s->work_start, caller), "record work_start");
   PACE_HIP(hipStreamWaitEvent(stream, s->work_start, 0), "wait work_start");
-  char* host = static_cast<char*>(host_buf);
   const int S = s->num_slots;
-  const bool host_kernel = device_addressable_host(host_buf, regions * chunk_bytes);
   // A region's events order its reuse within a call and between calls of one
   // chunk size; a call with another chunk size (or host buffer) carves other
   // regions, so its first D2H copy waits for the previous call's last H2D

@@ -410,12 +410,15 @@ def test_roundtrip_orders_against_the_callers_stream(gpu, side):
     assert bad is None, bad
 
 
-def test_mixed_stager_calls_on_two_streams_without_synchronisation(gpu):
+@pytest.mark.parametrize("ks", [(2, 2, 2, 2), (6, 2, 6, 2), (2, 6, 2, 6)],
+                         ids=["all-chunked", "one-chunk-first", "one-chunk-second"])
+def test_mixed_stager_calls_on_two_streams_without_synchronisation(gpu, ks):
     """One stager's slots and events order every kind of call against the
     others: a round trip on stream A, a pack to host on stream B, an unpack
     from host on stream A and a round trip on stream B, enqueued back to back
     with no synchronisation (the four calls move independent data), all end
-    exact."""
+    exact, also when some calls are one chunk (whose stages all run on the
+    caller's stream) and the others three."""
     L, pages, shape, n, k = 6, 48, (2, 16, 2, 64), 40, 2
     page_bytes = int(np.prod(shape)) * 2
     rng = np.random.default_rng(950)
@@ -430,15 +433,15 @@ def test_mixed_stager_calls_on_two_streams_without_synchronisation(gpu):
     host_in = torch.stack([s[torch.tensor(s_ids[2], device=gpu)] for s in srcs[2]]).cpu().pin_memory()
     streams = [torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)]
     torch.cuda.synchronize()
-    with ops.Stager(k * n * page_bytes, 4) as st:
+    with ops.Stager(L * n * page_bytes, 4) as st:
         with torch.cuda.stream(streams[0]):
-            st.roundtrip(srcs[0], s_ids[0], dsts[0], d_ids[0], ring[0], k)
+            st.roundtrip(srcs[0], s_ids[0], dsts[0], d_ids[0], ring[0], ks[0])
         with torch.cuda.stream(streams[1]):
-            st.pack_to_host(srcs[1], s_ids[1], host_out, k)
+            st.pack_to_host(srcs[1], s_ids[1], host_out, ks[1])
         with torch.cuda.stream(streams[0]):
-            st.unpack_from_host(host_in, dsts[2], d_ids[2], k)
+            st.unpack_from_host(host_in, dsts[2], d_ids[2], ks[2])
         with torch.cuda.stream(streams[1]):
-            st.roundtrip(srcs[3], s_ids[3], dsts[3], d_ids[3], ring[1], k)
+            st.roundtrip(srcs[3], s_ids[3], dsts[3], d_ids[3], ring[1], ks[3])
         torch.cuda.synchronize()
     for i in (0, 2, 3):
         bad = workloads.migration_mismatch(srcs[i], dsts[i], torch.tensor(s_ids[i], device=gpu),
@@ -446,6 +449,36 @@ def test_mixed_stager_calls_on_two_streams_without_synchronisation(gpu):
         assert bad is None, f"call {i}: {bad}"
     want = torch.stack([s[torch.tensor(s_ids[1], device=gpu)] for s in srcs[1]]).cpu()
     assert torch.equal(words(host_out), words(want)), "call 1: pack to host"
+
+
+@pytest.mark.parametrize("ks", [(2, 6, 2, 6), (6, 2, 6, 2), (2, 2, 2, 2), (6, 6, 6, 6)],
+                         ids=["chunked-first", "one-chunk-first", "all-chunked", "all-one-chunk"])
+def test_roundtrips_into_the_same_pages_land_in_call_order(gpu, ks):
+    """Round trips on one stager run their unpacks in call order whichever
+    stream each names: four calls enqueued back to back with no
+    synchronisation, alternating two streams, each writing other source
+    pages into the same destination pages, leave the last call's pages, also
+    when one-chunk calls (on the caller's stream) and three-chunk calls (on
+    the stager's streams) alternate."""
+    L, pages, shape, n = 6, 64, (2, 16, 2, 64), 40
+    page_bytes = int(np.prod(shape)) * 2
+    rng = np.random.default_rng(970)
+    srcs = [rand_pool(L, pages, shape, torch.bfloat16, gpu, 970 + i) for i in range(4)]
+    dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 979)
+    s_ids = [rng.permutation(pages)[:n].tolist() for _ in range(4)]
+    d_ids = rng.permutation(pages)[:n].tolist()
+    rings = [torch.empty(L * n * page_bytes, dtype=torch.uint8, pin_memory=True) for _ in range(4)]
+    streams = [torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)]
+    torch.cuda.synchronize()
+    with ops.Stager(L * n * page_bytes, 3) as st:
+        for i in range(4):
+            with torch.cuda.stream(streams[i % 2]):
+                st.roundtrip(srcs[i], s_ids[i], dst, d_ids, rings[i], ks[i])
+        torch.cuda.synchronize()
+    d_dev = torch.tensor(d_ids, device=gpu)
+    s_dev = torch.tensor(s_ids[3], device=gpu)
+    for l in range(L):
+        assert torch.equal(words(dst[l][d_dev]), words(srcs[3][l][s_dev])), f"layer {l}"
 
 
 def test_roundtrip_failing_part_way_leaves_the_stager_usable(gpu):
