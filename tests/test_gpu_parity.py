@@ -481,14 +481,16 @@ def test_roundtrips_into_the_same_pages_land_in_call_order(gpu, ks):
         assert torch.equal(words(dst[l][d_dev]), words(srcs[3][l][s_dev])), f"layer {l}"
 
 
-def test_roundtrip_failing_part_way_leaves_the_stager_usable(gpu):
+@pytest.mark.parametrize("k", [2, 6], ids=["three-chunks", "one-chunk"])
+def test_roundtrip_failing_part_way_leaves_the_stager_usable(gpu, k):
     """A round trip whose destination table has a NULL pointer for the last
     layer fails when it reaches that layer's chunk, on the host, after the
     earlier chunks were packed, copied and unpacked (the NULL pointer never
     reaches a kernel).  The call returns PACE_KV_EINVAL naming the layer, the
     earlier chunks' destination layers are exact, the later ones untouched,
-    and the same stager then runs a full round trip exactly."""
-    L, pages, shape, n, k = 6, 64, (2, 16, 2, 64), 40, 2
+    and the same stager then runs a full round trip exactly.  With one chunk
+    (every stage on the caller's stream) no destination layer changes."""
+    L, pages, shape, n = 6, 64, (2, 16, 2, 64), 40
     page_bytes = int(np.prod(shape)) * 2
     src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 900)
     dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 901)
@@ -508,7 +510,8 @@ def test_roundtrip_failing_part_way_leaves_the_stager_usable(gpu):
                                    host.numel(), None, ops._stream_handle(gpu))
         torch.cuda.synchronize()
         assert rc == _native.PACE_KV_EINVAL
-        assert "layer 1 pointer is NULL" in lib.pace_kv_last_error().decode()   # layer 1 of the last chunk
+        # the last layer's index within its chunk
+        assert f"layer {k - 1} pointer is NULL" in lib.pace_kv_last_error().decode()
         want = [words(b).clone() for b in before]
         for l in range(L - k):
             want[l][d_dev.long()] = words(src[l])[s_dev.long()]
