@@ -336,6 +336,21 @@ struct WorkJoin {
   }
 };
 
+// Makes `stream` wait for the copies a one-way leg enqueued on its copy
+// stream `side` when the leg fails part-way (best effort: the call is failing
+// already), so that the caller's stream is ordered after every copy of the
+// caller's host buffer.  The success path orders `stream` itself (ok).
+struct SideJoin {
+  hipStream_t side;
+  hipStream_t stream;
+  hipEvent_t event;
+  bool ok = false;
+  ~SideJoin() {
+    if (ok) return;
+    if (hipEventRecord(event, side) == hipSuccess) (void)hipStreamWaitEvent(stream, event, 0);
+  }
+};
+
 }  // namespace
 
 extern "C" {
@@ -404,11 +419,14 @@ int pace_kv_pack_to_host(pace_kv_stager* s, const void* const* src_layers, int n
     // us less per call for 2-8 MiB requests, about 1% less at 128 MiB).
     PACE_HIP(hipStreamWaitEvent(stream, s->out_free[0], 0), "wait out slot");
     PACE_KV_TRY(pack_chunk(s, p, 0, src_layers, pool_pages, page_ids, err_count, stream));
-    PACE_HIP(hipMemcpyAsync(host_out, s->out_ring, p.count(0) * p.layer_bytes, hipMemcpyDeviceToHost, stream),
-             "D2H copy");
+    // out_free follows the pack also when the copy fails to enqueue.
+    const hipError_t d2h =
+        hipMemcpyAsync(host_out, s->out_ring, p.count(0) * p.layer_bytes, hipMemcpyDeviceToHost, stream);
     PACE_HIP(hipEventRecord(s->out_free[0], stream), "record out_free");
+    PACE_HIP(d2h, "D2H copy");
     return PACE_KV_OK;
   }
+  SideJoin join{s->d2h, stream, s->d2h_done};
   // Step i enqueues pack(i + 1), then the copy of chunk i: the copy's
   // completion record, which holds back whatever follows it when the D2H
   // stream shares the caller's hardware queue, then only delays pack(i + 2).
@@ -433,6 +451,7 @@ int pace_kv_pack_to_host(pace_kv_stager* s, const void* const* src_layers, int n
   }
   PACE_HIP(hipEventRecord(s->d2h_done, s->d2h), "record d2h_done");
   PACE_HIP(hipStreamWaitEvent(stream, s->d2h_done, 0), "join D2H");
+  join.ok = true;
   return PACE_KV_OK;
 }
 
@@ -460,6 +479,8 @@ int pace_kv_unpack_from_host(pace_kv_stager* s, const void* host_in, void* const
   // The caller's earlier work (e.g. writes of host_in by a kernel) comes first.
   PACE_HIP(hipEventRecord(s->start, stream), "record start");
   PACE_HIP(hipStreamWaitEvent(s->h2d, s->start, 0), "wait start");
+  // On success the last unpack, on `stream`, follows every copy.
+  SideJoin join{s->h2d, stream, s->start};
   // Step i enqueues the copy of chunk i + 1, then unpack(i), whose wait for
   // chunk i's copy then holds back (on a shared hardware queue) only the copy
   // of chunk i + 2.  That copy refills the slot of chunk i + 2 - num_slots,
@@ -482,6 +503,7 @@ int pace_kv_unpack_from_host(pace_kv_stager* s, const void* host_in, void* const
       PACE_HIP(hipEventRecord(s->in_free[slot], stream), "record in_free");
     }
   }
+  join.ok = true;
   return PACE_KV_OK;
 }
 
@@ -518,8 +540,10 @@ int pace_kv_roundtrip(pace_kv_stager* s, const void* const* src_layers, int64_t 
     PACE_HIP(hipStreamWaitEvent(caller, s->out_free[0], 0), "wait out slot");
     PACE_HIP(hipStreamWaitEvent(caller, s->h2d_done, 0), "wait previous round trip");
     PACE_KV_TRY(pack_chunk(s, p, 0, src_layers, src_pool_pages, src_ids, err_count, caller));
-    PACE_HIP(copy_to_host(host, s->out_ring, bytes, host_kernel, caller), "D2H copy");
+    // out_free follows the pack also when the copy fails to enqueue.
+    const hipError_t d2h = copy_to_host(host, s->out_ring, bytes, host_kernel, caller);
     PACE_HIP(hipEventRecord(s->out_free[0], caller), "record out_free");
+    PACE_HIP(d2h, "D2H copy");
     PACE_HIP(hipStreamWaitEvent(caller, s->in_free[0], 0), "wait in slot");
     PACE_HIP(hipMemcpyAsync(s->in_ring, host, bytes, hipMemcpyHostToDevice, caller), "H2D copy");
     PACE_HIP(hipEventRecord(s->h2d_done, caller), "record h2d_done");

@@ -395,11 +395,13 @@ class Stager:
         ids = device_ids(page_ids, pool.device)
         n = ids.numel()
         self._host(host_out, pool, le - lb, n, "pack_to_host")
-        _native.check(_native.load().pace_kv_pack_to_host(
-            self._require(), pool.table(lb), le - lb, pool.num_pages, ids.data_ptr() if n else None,
-            n, pool.page_bytes, int(layers_per_chunk), host_out.data_ptr(), _err_ptr(err),
-            _stream_handle(pool.device)))
-        self._keep(host_out, ids)
+        try:
+            _native.check(_native.load().pace_kv_pack_to_host(
+                self._require(), pool.table(lb), le - lb, pool.num_pages, ids.data_ptr() if n else None,
+                n, pool.page_bytes, int(layers_per_chunk), host_out.data_ptr(), _err_ptr(err),
+                _stream_handle(pool.device)))
+        finally:  # a call failing part-way leaves copies in flight too
+            self._keep(host_out, ids)
         return host_out
 
     def unpack_from_host(self, host_in: torch.Tensor, dst, page_ids: IdsLike, layers_per_chunk: int,
@@ -410,11 +412,13 @@ class Stager:
         ids = device_ids(page_ids, pool.device, distinct=True)
         n = ids.numel()
         self._host(host_in, pool, le - lb, n, "unpack_from_host")
-        _native.check(_native.load().pace_kv_unpack_from_host(
-            self._require(), host_in.data_ptr(), pool.table(lb), le - lb, pool.num_pages,
-            ids.data_ptr() if n else None, n, pool.page_bytes, int(layers_per_chunk), _err_ptr(err),
-            _stream_handle(pool.device)))
-        self._keep(host_in, ids)
+        try:
+            _native.check(_native.load().pace_kv_unpack_from_host(
+                self._require(), host_in.data_ptr(), pool.table(lb), le - lb, pool.num_pages,
+                ids.data_ptr() if n else None, n, pool.page_bytes, int(layers_per_chunk), _err_ptr(err),
+                _stream_handle(pool.device)))
+        finally:
+            self._keep(host_in, ids)
 
     def roundtrip(self, src, src_ids: IdsLike, dst, dst_ids: IdsLike, host_buf: torch.Tensor,
                   layers_per_chunk: int, *, err: Optional[torch.Tensor] = None) -> None:
@@ -428,12 +432,14 @@ class Stager:
         n = s_ids.numel()
         if host_buf.device.type != "cpu" or not host_buf.is_contiguous():
             raise ValueError("roundtrip: host buffer must be a contiguous CPU tensor")
-        _native.check(_native.load().pace_kv_roundtrip(
-            self._require(), sp.table(), sp.num_pages, s_ids.data_ptr() if n else None, dp.table(),
-            dp.num_pages, d_ids.data_ptr() if n else None, sp.num_layers, n, sp.page_bytes,
-            int(layers_per_chunk), host_buf.data_ptr(), host_buf.numel() * host_buf.element_size(),
-            _err_ptr(err), _stream_handle(sp.device)))
-        self._keep(host_buf, s_ids, d_ids)
+        try:
+            _native.check(_native.load().pace_kv_roundtrip(
+                self._require(), sp.table(), sp.num_pages, s_ids.data_ptr() if n else None, dp.table(),
+                dp.num_pages, d_ids.data_ptr() if n else None, sp.num_layers, n, sp.page_bytes,
+                int(layers_per_chunk), host_buf.data_ptr(), host_buf.numel() * host_buf.element_size(),
+                _err_ptr(err), _stream_handle(sp.device)))
+        finally:
+            self._keep(host_buf, s_ids, d_ids)
 
     def close(self) -> None:
         if self._handle is not None:

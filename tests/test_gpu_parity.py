@@ -525,6 +525,61 @@ def test_roundtrip_failing_part_way_leaves_the_stager_usable(gpu, k):
         assert bad is None, bad
 
 
+@pytest.mark.parametrize("k", [2, 6], ids=["three-chunks", "one-chunk"])
+def test_one_way_legs_failing_part_way_leave_the_stager_usable(gpu, k):
+    """A pack to host whose source table, and an unpack from host whose
+    destination table, has a NULL pointer for the last layer fail with
+    PACE_KV_EINVAL when they reach that layer's chunk (c).  What was enqueued
+    before it arrives exactly, and nothing else: the pack has copied chunks
+    0..c-2 (step i enqueues pack(i+1) before the copy of chunk i), the unpack
+    has written chunks 0..c-1.  The caller's stream is ordered after the
+    copies already enqueued, and the same stager then runs both legs
+    exactly."""
+    L, pages, shape, n = 6, 64, (2, 16, 2, 64), 40
+    page_bytes = int(np.prod(shape)) * 2
+    src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 930)
+    dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 931)
+    before = [d.clone() for d in dst]
+    rng = np.random.default_rng(930)
+    s_dev = torch.tensor(rng.permutation(pages)[:n].tolist(), dtype=torch.int32, device=gpu)
+    d_dev = torch.tensor(rng.permutation(pages)[:n].tolist(), dtype=torch.int32, device=gpu)
+    want = torch.stack([words(s)[s_dev.long()] for s in src])      # [L, n, ...] int16 words
+    host = torch.zeros((L, n) + shape, dtype=torch.bfloat16, pin_memory=True)
+    host_in = want.view(torch.bfloat16).cpu().pin_memory()
+    bad_src = _native.pointer_array([t.data_ptr() for t in src[:-1]] + [None])
+    bad_dst = _native.pointer_array([t.data_ptr() for t in dst[:-1]] + [None])
+    lib = _native.load()
+    stream = ops._stream_handle(gpu)
+    with ops.Stager(k * n * page_bytes, 3) as st:
+        rc = lib.pace_kv_pack_to_host(st._handle, ctypes.addressof(bad_src), L, pages, s_dev.data_ptr(), n,
+                                      page_bytes, k, host.data_ptr(), None, stream)
+        torch.cuda.synchronize()
+        assert rc == _native.PACE_KV_EINVAL
+        assert f"layer {k - 1} pointer is NULL" in lib.pace_kv_last_error().decode()
+        c = (L - 1) // k                # the failing chunk
+        done = max(0, c - 1) * k         # layers copied to the host
+        assert torch.equal(words(host)[:done], want[:done].cpu())
+        assert not words(host)[done:].any()
+        rc = lib.pace_kv_unpack_from_host(st._handle, host_in.data_ptr(), ctypes.addressof(bad_dst), L, pages,
+                                          d_dev.data_ptr(), n, page_bytes, k, None, stream)
+        torch.cuda.synchronize()
+        assert rc == _native.PACE_KV_EINVAL
+        for l in range(L):
+            expect = words(before[l]).clone()
+            if l < c * k:                # layers unpacked
+                expect[d_dev.long()] = want[l]
+            assert torch.equal(words(dst[l]), expect), f"layer {l} after the failed unpack"
+        out = torch.empty((L, n) + shape, dtype=torch.bfloat16, pin_memory=True)
+        st.pack_to_host(src, s_dev, out, k)
+        dst2 = rand_pool(L, pages, shape, torch.bfloat16, gpu, 932)
+        before2 = [d.clone() for d in dst2]
+        st.unpack_from_host(host_in, dst2, d_dev, k)
+        torch.cuda.synchronize()
+        assert torch.equal(words(out), want.cpu())
+        bad = workloads.migration_mismatch(src, dst2, s_dev, d_dev, before2)
+        assert bad is None, bad
+
+
 def _hip_host_alloc(nbytes):
     """hipHostMalloc of exactly nbytes, as (uint8 CPU tensor over it, free):
     the caller synchronises and drops every view before calling free()."""
