@@ -168,8 +168,9 @@ int pace_kv_stager_destroy(pace_kv_stager* stager);
  * layout [num_layers, n_pages, page_size-slice...] of PACK with
  * out_layer_stride = n_pages * page_bytes.  Pinned host memory gives
  * asynchronous DMA; pageable memory works but the runtime stages it.
- * When the call returns, `stream` is ordered after the last copy.  A call of
- * one chunk (layers_per_chunk >= num_layers) packs and copies on `stream`.
+ * When the call returns, `stream` is ordered after the last copy enqueued,
+ * also when it fails part-way.  A call of one chunk
+ * (layers_per_chunk >= num_layers) packs and copies on `stream`.
  *
  * Replaces the gather + pageable device-to-host copy loop of
  * KVhelper.get_kv_cache (paceserve/kv_transfer/kv_utils.py:44-47).
@@ -184,7 +185,9 @@ int pace_kv_pack_to_host(pace_kv_stager* stager,
 /*
  * Unpack from host memory: the mirror of pace_kv_pack_to_host.  Chunk c is
  * copied host-to-device on the H2D side stream while chunk c-1 is unpacked on
- * `stream`; a call of one chunk copies and unpacks on `stream`.
+ * `stream`; a call of one chunk copies and unpacks on `stream`.  When the
+ * call returns, `stream` is ordered after every copy it enqueued, also when
+ * it fails part-way.
  *
  * Replaces the pageable host-to-device copy + scatter loop of
  * KVhelper.insert_kv_cache (paceserve/kv_transfer/kv_utils.py:49-52).
