@@ -491,7 +491,9 @@ def run_dropin(dev, steps: int = 10, warmup: int = 2) -> dict:
     pageable torch.zeros host tensor filled layer by layer from
     gpu_cache[i][tensor(ids)] (paceserve/kv_transfer/kv_utils.py:44-46), then
     gpu_cache[i][tensor(ids)] = content[i].to(device) per layer (:51-52).
-    Wall-clock per call pair, to completion; both must leave the same bytes."""
+    Wall-clock per call pair, to completion; both must leave the same bytes.
+    The same for the request's first 1 and 32 pages (16 and 512 tokens), where
+    fixed costs per call weigh more (`small`)."""
     import torch
 
     from paceserve_amd import workloads
@@ -516,46 +518,56 @@ def run_dropin(dev, steps: int = 10, warmup: int = 2) -> dict:
     class _Seq:
         seq_id = "r"
 
-    class _Tables:
-        def _get_block_table(self, seq):
-            return ids
-
     src_h, dst_h = helper(src), helper(dst)
 
-    def ours():
-        content, _ = src_h.get_kv_cache(_Seq(), _Tables())
-        if not dst_h.insert_kv_cache(content, dst_ids, dev):
-            raise RuntimeError("insert_kv_cache failed")
+    def measure(ids, dst_ids, out, what):
+        n = len(ids)
+        payload = L * n * w.shape.page_bytes
 
-    def reference():
-        seq_cache = torch.zeros((L, n) + w.shape.page_shape, dtype=w.shape.dtype)
-        for i in range(L):
-            seq_cache[i] = src[i][torch.tensor(ids), :, :, :, :]
-        for i in range(L):
-            dst[i][torch.tensor(dst_ids), :, :, :, :] = seq_cache[i].to(dev)
+        class _Tables:
+            def _get_block_table(self, seq):
+                return ids
 
-    out = {"payload_bytes": w.payload_bytes, "workload": w.name, "runs": steps}
-    for name, fn in (("kvhelper", ours), ("reference_torch", reference)):
-        ts = []
-        for i in range(warmup + steps):
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            fn()
-            torch.cuda.synchronize()
-            if i >= warmup:
-                ts.append(time.perf_counter() - t0)
-        ms = statistics.median(ts) * 1e3
-        out[f"{name}_ms"] = round(ms, 2)
-        out[f"{name}_gbs_per_direction"] = round(w.payload_bytes / (ms / 1e3) / 1e9, 2)
-        log(f"drop-in {name}: {ms:.2f} ms per get + insert")
-        if name == "kvhelper":
-            after = [d[torch.tensor(dst_ids, device=dev)].view(torch.int16).clone() for d in dst]
-            for d in dst:
-                d.zero_()
-    ok = all(torch.equal(d[torch.tensor(dst_ids, device=dev)].view(torch.int16), a) for d, a in zip(dst, after))
-    ok = ok and all(torch.equal(s[torch.tensor(ids, device=dev)].view(torch.int16), a) for s, a in zip(src, after))
-    out["same_bytes"] = ok
-    out["speedup"] = round(out["reference_torch_ms"] / out["kvhelper_ms"], 2)
+        def ours():
+            content, _ = src_h.get_kv_cache(_Seq(), _Tables())
+            if not dst_h.insert_kv_cache(content, dst_ids, dev):
+                raise RuntimeError("insert_kv_cache failed")
+
+        def reference():
+            seq_cache = torch.zeros((L, n) + w.shape.page_shape, dtype=w.shape.dtype)
+            for i in range(L):
+                seq_cache[i] = src[i][torch.tensor(ids), :, :, :, :]
+            for i in range(L):
+                dst[i][torch.tensor(dst_ids), :, :, :, :] = seq_cache[i].to(dev)
+
+        for name, fn in (("kvhelper", ours), ("reference_torch", reference)):
+            ts = []
+            for i in range(warmup + steps):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                if i >= warmup:
+                    ts.append(time.perf_counter() - t0)
+            ms = statistics.median(ts) * 1e3
+            out[f"{name}_ms"] = round(ms, 3)
+            out[f"{name}_gbs_per_direction"] = round(payload / (ms / 1e3) / 1e9, 2)
+            log(f"drop-in {what} {name}: {ms:.3f} ms per get + insert")
+            if name == "kvhelper":
+                after = [d[torch.tensor(dst_ids, device=dev)].view(torch.int16).clone() for d in dst]
+                for d in dst:
+                    d.zero_()
+        ok = all(torch.equal(d[torch.tensor(dst_ids, device=dev)].view(torch.int16), a) for d, a in zip(dst, after))
+        ok = ok and all(torch.equal(s[torch.tensor(ids, device=dev)].view(torch.int16), a) for s, a in zip(src, after))
+        out["same_bytes"] = ok
+        out["speedup"] = round(out["reference_torch_ms"] / out["kvhelper_ms"], 2)
+        return out
+
+    out = measure(ids, dst_ids, {"payload_bytes": w.payload_bytes, "workload": w.name, "runs": steps}, "4096 tok")
+    out["small"] = {}
+    for pages in (1, 32):
+        key = f"{pages * w.shape.page_size}tok"
+        out["small"][key] = measure(ids[:pages], dst_ids[:pages], {"payload_bytes": L * pages * w.shape.page_bytes}, key)
     return out
 
 
