@@ -136,16 +136,28 @@ def device_ids(ids: IdsLike, device: torch.device, distinct: bool = False) -> to
                 raise ValueError(f"page ids on {ids.device}, pool on {device}")
             return ids
         host = ids.to(torch.int32).contiguous().view(-1)
+        if host.numel() == 0:
+            return torch.empty(0, dtype=torch.int32, device=device)
+        if distinct:
+            _check_distinct(host.numpy())
+        if not host.is_pinned():
+            host = host.pin_memory()
     else:
-        host = torch.tensor(list(ids), dtype=torch.int32)
-    if host.numel() == 0:
-        return torch.empty(0, dtype=torch.int32, device=device)
-    if distinct and host.numel() > 1:
-        u, c = np.unique(host.numpy(), return_counts=True)
+        ids = list(ids)
+        if not ids:
+            return torch.empty(0, dtype=torch.int32, device=device)
+        if distinct:
+            _check_distinct(np.asarray(ids))
+        host = torch.tensor(ids, dtype=torch.int32, pin_memory=True)
+    return host.to(device, non_blocking=True)
+
+
+def _check_distinct(ids: np.ndarray) -> None:
+    if ids.size > 1:
+        u, c = np.unique(ids, return_counts=True)
         if (c > 1).any():
             raise ValueError(f"destination page {int(u[c > 1][0])} appears more than once; destination page "
                              "ids must be distinct")
-    return host.pin_memory().to(device, non_blocking=True)
 
 
 def _err_ptr(err: Optional[torch.Tensor]) -> Optional[int]:
@@ -367,12 +379,19 @@ class Stager:
         self.slot_bytes = int(slot_bytes)
         self.num_slots = int(num_slots)
         self._inflight: list = []
+        self._spare: list = []  # events of finished calls, recorded again
 
     def _keep(self, *objs) -> None:
-        ev = torch.cuda.Event()
+        live = []
+        for e, o in self._inflight:
+            if e.query():
+                self._spare.append(e)
+            else:
+                live.append((e, o))
+        ev = self._spare.pop() if self._spare else torch.cuda.Event()
         ev.record(torch.cuda.current_stream(self.device))
-        self._inflight = [(e, o) for e, o in self._inflight if not e.query()]
-        self._inflight.append((ev, objs))
+        live.append((ev, objs))
+        self._inflight = live
 
     def _require(self):
         if self._handle is None:
@@ -447,6 +466,7 @@ class Stager:
             with torch.cuda.device(self.device):
                 _native.check(_native.load().pace_kv_stager_destroy(handle))
             self._inflight.clear()
+            self._spare.clear()
 
     def __enter__(self):
         return self
