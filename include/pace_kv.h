@@ -170,7 +170,8 @@ int pace_kv_stager_destroy(pace_kv_stager* stager);
  * asynchronous DMA; pageable memory works but the runtime stages it.
  * When the call returns, `stream` is ordered after the last copy enqueued,
  * also when it fails part-way.  A call of one chunk
- * (layers_per_chunk >= num_layers) packs and copies on `stream`.
+ * (layers_per_chunk >= num_layers) packs and copies on `stream`, the copy by
+ * a 16-wave kernel when host_out is pinned memory the device addresses.
  *
  * Replaces the gather + pageable device-to-host copy loop of
  * KVhelper.get_kv_cache (paceserve/kv_transfer/kv_utils.py:44-47).

@@ -591,20 +591,21 @@ def _hip_host_alloc(nbytes):
     return torch.from_numpy(arr), lambda: hip.hipHostFree(ptr)
 
 
+@pytest.mark.parametrize("k", [2, 6], ids=["three-chunks", "one-chunk"])
 @pytest.mark.parametrize("kind", ["pageable", "pinned-at-offset", "pinned-to-the-end"])
-def test_roundtrip_host_buffer_kinds(gpu, kind):
-    """The round trip copies device to host with a kernel when the host
-    buffer is pinned memory the device addresses, and with hipMemcpyAsync
-    otherwise.  A pageable buffer, a pinned view starting 4 KiB into its
-    allocation, and a pinned view ending exactly at its allocation's end all
-    give the exact destination, two calls in a row; the second call's chunks
-    (656 KiB) are not a multiple of the kernel's 256 KiB pass, so its
-    remainder loop runs."""
+def test_roundtrip_host_buffer_kinds(gpu, kind, k):
+    """The round trip, and a one-chunk pack to host, copy device to host with
+    a kernel when the host buffer is pinned memory the device addresses, and
+    with hipMemcpyAsync otherwise.  A pageable buffer, a pinned view starting
+    4 KiB into its allocation, and a pinned view ending exactly at its
+    allocation's end all give the exact destination (and host bytes), two
+    calls in a row; the second call's chunks (656 KiB per layer) are not a
+    multiple of the kernel's 256 KiB pass, so its remainder loop runs."""
     L, pages, shape = 6, 64, (2, 16, 2, 64)
     page_bytes = int(np.prod(shape)) * 2
     src = rand_pool(L, pages, shape, torch.bfloat16, gpu, 800)
     rng = np.random.default_rng(800)
-    with ops.Stager(4 * 48 * page_bytes, 4) as st:
+    with ops.Stager(6 * 48 * page_bytes, 4) as st:
         for rep in range(2):
             n = 48 - rep * 7
             need = L * n * page_bytes
@@ -621,8 +622,14 @@ def test_roundtrip_host_buffer_kinds(gpu, kind):
             d_ids = rng.permutation(pages)[:n].tolist()
             dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 801 + rep)
             before = [d.clone() for d in dst]
+            want = torch.stack([words(s)[torch.tensor(s_ids, device=gpu)] for s in src]).cpu()
             try:
-                st.roundtrip(src, s_ids, dst, d_ids, host, 2)
+                st.roundtrip(src, s_ids, dst, d_ids, host, k)
+                torch.cuda.synchronize()   # the round trip reads host until it completes
+                host.zero_()
+                st.pack_to_host(src, s_ids, host.view(torch.bfloat16).view((L, n) + shape), k)
+                torch.cuda.synchronize()
+                packed = host.view(torch.int16).view(want.shape).clone()
             finally:
                 torch.cuda.synchronize()
                 if free is not None:
@@ -632,6 +639,7 @@ def test_roundtrip_host_buffer_kinds(gpu, kind):
             bad = workloads.migration_mismatch(src, dst, torch.tensor(s_ids, device=gpu),
                                                torch.tensor(d_ids, device=gpu), before)
             assert bad is None, f"{kind} rep {rep}: {bad}"
+            assert torch.equal(packed, want), f"{kind} rep {rep}: pack to host"
 
 
 @pytest.mark.parametrize("seed", range(16))
