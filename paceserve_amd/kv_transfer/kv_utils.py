@@ -95,17 +95,23 @@ def roundtrip_chunk_layers(num_layers: int, layer_bytes: int) -> int:
     layers giving chunks of 8 MiB and more when a request has at most 8 of
     them, 32 MiB and more up to 16 of them, or 128 MiB and more at any count,
     which keeps the pipeline out of the regime where many small chunks stall
-    it (16 chunks of 4-8 MiB, or 32 chunks, ran at 5-37 GB/s per direction).
-    Measured on MI355X on stagers created once and kept (32 layers, 64 KiB
-    pages): for 256-1024-token requests the chosen 8-16 MiB chunks ran 2-5%
-    faster than chunks twice as large (32-41 GB/s), and for 2048-8192 tokens
-    the choice was the fastest measured or within 1.4% of it (42-46 GB/s)."""
+    it (16 chunks of 4-8 MiB, or 32 chunks, ran at 5-37 GB/s per direction);
+    then as few layers as keep that many chunks, so that the chunks are as
+    even as whole layers allow.  Measured on MI355X on stagers created once
+    and kept (32 layers, 64 KiB pages): for 256-1024-token requests the chosen
+    8-16 MiB chunks ran 2-5% faster than chunks twice as large (32-41 GB/s),
+    and for 2048-8192 tokens the choice was the fastest measured or within
+    1.4% of it (42-46 GB/s).  Evening out the chunks matters where the first
+    count leaves a short last chunk: a 10 MiB request in chunks of 26 and 6
+    layers took 562 us, in two of 16 layers 437 us (the first chunk's D2H copy
+    and the last one's H2D copy each run alone), and 18-20 MiB requests in
+    three chunks ran 3-5% faster as 11 + 11 + 10 layers than as 15 + 15 + 2."""
     if layer_bytes <= 0:
         return max(1, num_layers)
     for k in range(1, num_layers + 1):
         chunk, count = k * layer_bytes, -(-num_layers // k)
         if chunk >= 128 * MiB or (chunk >= 32 * MiB and count <= 16) or (chunk >= 8 * MiB and count <= 8):
-            return k
+            return -(-num_layers // count)
     return max(1, num_layers)
 
 

@@ -161,10 +161,17 @@ def test_roundtrip_chunk_layers_avoid_many_small_chunks():
     assert roundtrip_chunk_layers(32, 3 * MiB) == 4       # 12 MiB: 3 layers would make 11 chunks
     assert roundtrip_chunk_layers(32, MiB // 4) == 32     # 8 MiB in all: one chunk
     assert roundtrip_chunk_layers(80, 16 * MiB) == 5      # 80-layer cache: 16 chunks of 80 MiB
+    # chunks evened out: two chunks of 16 layers, not 26 + 6 (or 22 + 10) ...
+    assert roundtrip_chunk_layers(32, 5 * 64 * 1024) == 16
+    assert roundtrip_chunk_layers(32, 6 * 64 * 1024) == 16
+    # ... and three of 11, 11 and 10 layers, not 15 + 15 + 2
+    assert roundtrip_chunk_layers(32, 9 * 64 * 1024) == 11
     for layers in (1, 7, 32, 80):
-        for mib in (1, 3, 8, 40, 300):
-            k = roundtrip_chunk_layers(layers, mib * MiB)
+        for kib in (64, 320, 576, 1024, 3072, 8192, 40960, 307200):
+            k = roundtrip_chunk_layers(layers, kib * 1024)
             assert 1 <= k <= layers
+            # no fewer layers per chunk give the same number of chunks
+            assert k == 1 or -(-layers // (k - 1)) > -(-layers // k)
 
 
 class _FakeHelper:
