@@ -213,7 +213,9 @@ int pace_kv_unpack_from_host(pace_kv_stager* stager, const void* host_in,
  * scratch array of PACE_KV_NOALLOC_SCRATCH_BYTES, which the library holds on
  * every GPU it runs on until the process ends, and copied from there to
  * host_out, pack and copy both on `stream` (no side stream, so a chunk's pack
- * does not overlap the previous chunk's copy).  Chunks are whole layers when
+ * does not overlap the previous chunk's copy); the copy is a 16-wave kernel
+ * when the device addresses host_out at the same pointer (hipHostMalloc's
+ * default), else hipMemcpyAsync.  Chunks are whole layers when
  * one layer's n_pages * page_bytes fits the scratch, else runs of pages of
  * one layer; a page larger than the scratch is rejected (PACE_KV_ERANGE).
  * host_out must be pinned host memory (hipHostMalloc) and host_out_bytes the

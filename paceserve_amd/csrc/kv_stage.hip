@@ -697,6 +697,10 @@ int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers, 
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   char* host = static_cast<char*>(host_out);
   const int64_t layer_bytes = n_pages * page_bytes;
+  // The copies are the copy kernel's when the device addresses host_out at
+  // the same pointer (hipHostMalloc's default), which follows each pack
+  // sooner than a DMA copy does.
+  const bool kernel = device_addressable_host(host_out, payload);
   // Every pack and copy runs on `stream`, so a chunk's pack overwrites the
   // scratch only after the previous chunk's copy has read it.
   if (layer_bytes <= cap) {
@@ -707,8 +711,7 @@ int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers, 
       const int nl = num_layers - l0 < k ? num_layers - l0 : k;
       PACE_KV_TRY(pace_kv_pack(src_layers + l0, nl, pool_pages, page_ids, n_pages, page_bytes, slot,
                                layer_bytes, err_count, stream));
-      PACE_HIP(hipMemcpyAsync(host + l0 * layer_bytes, slot, nl * layer_bytes, hipMemcpyDeviceToHost, stream),
-               "D2H copy");
+      PACE_HIP(copy_to_host(host + l0 * layer_bytes, slot, nl * layer_bytes, kernel, stream), "D2H copy");
     }
   } else {
     // runs of pages of one layer
@@ -718,8 +721,7 @@ int pace_kv_pack_to_host_noalloc(const void* const* src_layers, int num_layers, 
         const int64_t np = n_pages - p0 < run ? n_pages - p0 : run;
         PACE_KV_TRY(pace_kv_pack(src_layers + l, 1, pool_pages, page_ids + p0, np, page_bytes, slot,
                                  np * page_bytes, err_count, stream));
-        PACE_HIP(hipMemcpyAsync(host + l * layer_bytes + p0 * page_bytes, slot, np * page_bytes,
-                                hipMemcpyDeviceToHost, stream),
+        PACE_HIP(copy_to_host(host + l * layer_bytes + p0 * page_bytes, slot, np * page_bytes, kernel, stream),
                  "D2H copy");
       }
     }
