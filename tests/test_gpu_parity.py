@@ -481,6 +481,64 @@ def test_roundtrips_into_the_same_pages_land_in_call_order(gpu, ks):
         assert torch.equal(words(dst[l][d_dev]), words(srcs[3][l][s_dev])), f"layer {l}"
 
 
+def test_random_call_sequences_on_three_streams(gpu):
+    """Seeded random sequences of 3-7 calls on one stager (pack to host,
+    unpack from host, round trip; 1, 2, 3 or 6 layers per chunk, so one chunk
+    or several) spread over three streams with no synchronisation between
+    them.  Every call's bytes are exact, and round trips into one shared
+    destination leave the last one's pages."""
+    L, pages, shape, n = 6, 64, (2, 16, 2, 64), 24
+    page_bytes = int(np.prod(shape)) * 2
+    streams = [torch.cuda.Stream(gpu) for _ in range(3)]
+    srcs = [rand_pool(L, pages, shape, torch.bfloat16, gpu, 500 + i) for i in range(4)]
+    with ops.Stager(L * n * page_bytes, 3) as st:
+        for it in range(40):
+            rng = np.random.default_rng(it)
+            shared = rand_pool(L, pages, shape, torch.bfloat16, gpu, 900 + it)
+            shared_ids = rng.permutation(pages)[:n].tolist()
+            last, checks, keep = None, [], []
+            torch.cuda.synchronize()
+            for c in range(int(rng.integers(3, 8))):
+                kind = str(rng.choice(["pack", "unpack", "roundtrip", "shared"]))
+                k = int(rng.choice([1, 2, 3, 6]))
+                src = srcs[int(rng.integers(0, len(srcs)))]
+                s_ids = rng.permutation(pages)[:n].tolist()
+                d_ids = rng.permutation(pages)[:n].tolist()
+                want = torch.stack([words(t)[torch.tensor(s_ids, device=gpu)] for t in src])
+                ring = torch.empty(L * n * page_bytes, dtype=torch.uint8, pin_memory=True)
+                keep.append(ring)
+                with torch.cuda.stream(streams[int(rng.integers(0, 3))]):
+                    if kind == "pack":
+                        host = torch.zeros((L, n) + shape, dtype=torch.bfloat16, pin_memory=True)
+                        st.pack_to_host(src, s_ids, host, k)
+                        checks.append((kind, host, None, want))
+                    elif kind == "unpack":
+                        dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 700 + c)
+                        host = want.view(torch.bfloat16).cpu().pin_memory()
+                        keep.append(host)
+                        st.unpack_from_host(host, dst, d_ids, k)
+                        checks.append((kind, dst, d_ids, want))
+                    elif kind == "roundtrip":
+                        dst = rand_pool(L, pages, shape, torch.bfloat16, gpu, 800 + c)
+                        st.roundtrip(src, s_ids, dst, d_ids, ring, k)
+                        checks.append((kind, dst, d_ids, want))
+                    else:
+                        st.roundtrip(src, s_ids, shared, shared_ids, ring, k)
+                        last = want
+            torch.cuda.synchronize()
+            for kind, out, d_ids, want in checks:
+                if kind == "pack":
+                    assert torch.equal(words(out), want.cpu()), f"iteration {it}: pack to host"
+                else:
+                    di = torch.tensor(d_ids, device=gpu)
+                    for l in range(L):
+                        assert torch.equal(words(out[l])[di], want[l]), f"iteration {it}: {kind} layer {l}"
+            if last is not None:
+                di = torch.tensor(shared_ids, device=gpu)
+                for l in range(L):
+                    assert torch.equal(words(shared[l])[di], last[l]), f"iteration {it}: shared destination"
+
+
 @pytest.mark.parametrize("k", [2, 6], ids=["three-chunks", "one-chunk"])
 def test_roundtrip_failing_part_way_leaves_the_stager_usable(gpu, k):
     """A round trip whose destination table has a NULL pointer for the last
