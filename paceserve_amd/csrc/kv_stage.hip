@@ -34,15 +34,18 @@
 // and switched some of them, by rules of its own, to a DMA engine, where they
 // ran one after the other with the H2D copies (12.8 GB/s).  The round trip
 // therefore copies device to host with a kernel of its own, sized to leave
-// the CUs to the packs and unpacks (copy_to_host_kernel).  Its packs and unpacks run on a
-// work stream of the stager's own, which keeps them off whatever else the
-// caller's stream carries; measured against the caller's stream on stagers
-// kept for the whole run, it was 2% and 6% faster for 2048- and 4096-token
-// requests and within 2% either way for 256-1024 and 8192 tokens.
+// the CUs to the packs and unpacks (copy_to_host_kernel).  Its packs and
+// unpacks run on a work stream of the stager's own, which keeps them off
+// whatever else the caller's stream carries; measured against the caller's
+// stream on stagers kept for the whole run, it was 2% and 6% faster for 2048-
+// and 4096-token requests and within 2% either way for 256-1024 and 8192
+// tokens.
 //
 // A call whose layers fit one chunk has nothing to overlap, so all its stages
 // run on the caller's stream: each wait between streams adds latency, 30-36 us
-// per call on 2-8 MiB requests.
+// per call on 2-8 MiB requests.  Its device-to-host copy is the copy kernel
+// too, which follows a pack on the same stream sooner than a DMA copy does;
+// so is the allocation-free pack's.
 //
 // Device slots are reused round-robin; before a slot is overwritten, the
 // stream that writes it waits for the event recorded after the last read of
