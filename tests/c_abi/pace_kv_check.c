@@ -5,7 +5,10 @@
  * pages of the destination pool, and checks every byte on the host against a
  * plain memcpy restatement.  Then sends four pages through a cross-process
  * channel (both endpoints in this process: the message fits the ring) into
- * further destination pages, and checks them the same way.  Also checks that
+ * further destination pages, and checks them the same way.  Then moves the
+ * same pages through pinned host memory with a stager (pack to host, unpack
+ * from host, round trip), once with one chunk of all layers and once with a
+ * chunk per layer, checking the host bytes and both pools.  Also checks that
  * an argument error returns PACE_KV_EINVAL with a message.  Exit status 0
  * means every check passed.
  *
@@ -165,6 +168,85 @@ int main(void) {
     }
   }
 
+  /* through pinned host memory with a stager: pack to host, unpack from host
+     into stage pages, round trip into rt pages; one chunk, then a chunk per
+     layer, with the target pages zeroed before each pass */
+  {
+    const int32_t page_sets[2][N] = {{13, 6, 10, 15}, {0, 3, 5, 11}};
+    const size_t payload = (size_t)LAYERS * N * PAGE_BYTES;
+    const int chunks[2] = {LAYERS, 1};
+    pace_kv_stager* st = NULL;
+    void *pinned = NULL, *ids_sets[2] = {NULL, NULL};
+    int pass, s;
+    HIP_OK(hipHostMalloc(&pinned, payload, 0));
+    for (s = 0; s < 2; ++s) {
+      HIP_OK(hipMalloc(&ids_sets[s], sizeof(page_sets[s])));
+      HIP_OK(hipMemcpy(ids_sets[s], page_sets[s], sizeof(page_sets[s]), hipMemcpyHostToDevice));
+    }
+    rc = pace_kv_stager_create((int64_t)payload, 2, &st);
+    for (pass = 0; pass < 2 && rc == PACE_KV_OK; ++pass) {
+      const int32_t* stage_ids = page_sets[pass];
+      const int32_t* rt_ids = page_sets[1 - pass];
+      for (l = 0; l < LAYERS; ++l)
+        for (s = 0; s < 2; ++s)
+          for (j = 0; j < N; ++j) {
+            HIP_OK(hipMemset((char*)dst_layers[l] + (size_t)page_sets[s][j] * PAGE_BYTES, 0, PAGE_BYTES));
+            memset(host_dst[l] + (size_t)page_sets[s][j] * PAGE_BYTES, 0, PAGE_BYTES);
+          }
+      memset(pinned, 0, payload);
+      HIP_OK(hipDeviceSynchronize());
+      rc = pace_kv_pack_to_host(st, (const void* const*)src_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_src, N,
+                                PAGE_BYTES, chunks[pass], pinned, NULL, NULL);
+      if (rc == PACE_KV_OK) {
+        HIP_OK(hipDeviceSynchronize());
+        for (l = 0; l < LAYERS; ++l)
+          for (j = 0; j < N; ++j)
+            if (memcmp((unsigned char*)pinned + ((size_t)l * N + j) * PAGE_BYTES,
+                       host_src[l] + (size_t)src_ids[j] * PAGE_BYTES, PAGE_BYTES) != 0) {
+              fprintf(stderr, "pack to host, %d layers per chunk: layer %d page %d differs\n", chunks[pass], l, j);
+              ++failures;
+            }
+        rc = pace_kv_unpack_from_host(st, pinned, dst_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_sets[pass], N,
+                                      PAGE_BYTES, chunks[pass], NULL, NULL);
+      }
+      if (rc == PACE_KV_OK)
+        rc = pace_kv_roundtrip(st, (const void* const*)src_layers, POOL_PAGES, (const int32_t*)ids_src, dst_layers,
+                               POOL_PAGES, (const int32_t*)ids_sets[1 - pass], LAYERS, N, PAGE_BYTES, chunks[pass],
+                               pinned, (int64_t)payload, NULL, NULL);
+      if (rc != PACE_KV_OK) break;
+      HIP_OK(hipDeviceSynchronize());
+      for (l = 0; l < LAYERS; ++l) {
+        for (j = 0; j < N; ++j) {
+          memcpy(host_dst[l] + (size_t)stage_ids[j] * PAGE_BYTES, host_src[l] + (size_t)src_ids[j] * PAGE_BYTES,
+                 PAGE_BYTES);
+          memcpy(host_dst[l] + (size_t)rt_ids[j] * PAGE_BYTES, host_src[l] + (size_t)src_ids[j] * PAGE_BYTES,
+                 PAGE_BYTES);
+        }
+        HIP_OK(hipMemcpy(got, dst_layers[l], pool_bytes, hipMemcpyDeviceToHost));
+        if (memcmp(got, host_dst[l], pool_bytes) != 0) {
+          fprintf(stderr, "destination layer %d differs after staging with %d layers per chunk\n", l, chunks[pass]);
+          ++failures;
+        }
+        HIP_OK(hipMemcpy(got, src_layers[l], pool_bytes, hipMemcpyDeviceToHost));
+        if (memcmp(got, host_src[l], pool_bytes) != 0) {
+          fprintf(stderr, "source layer %d was written by staging\n", l);
+          ++failures;
+        }
+      }
+    }
+    if (rc != PACE_KV_OK) {
+      fprintf(stderr, "staging status %d: %s\n", rc, pace_kv_last_error());
+      return 1;
+    }
+    rc = pace_kv_stager_destroy(st);
+    if (rc != PACE_KV_OK) {
+      fprintf(stderr, "stager_destroy status %d: %s\n", rc, pace_kv_last_error());
+      return 1;
+    }
+    HIP_OK(hipHostFree(pinned));
+    for (s = 0; s < 2; ++s) HIP_OK(hipFree(ids_sets[s]));
+  }
+
   /* an argument error is caught on the host, before any launch */
   rc = pace_kv_pack((const void* const*)src_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_src, N, 100,
                     buf, (int64_t)N * PAGE_BYTES, NULL, NULL);
@@ -186,7 +268,7 @@ int main(void) {
   free(host_buf);
   free(got);
   if (failures) return 1;
-  printf("pace_kv C ABI check passed: %d layers x %d pages of %d B packed and unpacked, and sent through "
-         "a channel\n", LAYERS, N, PAGE_BYTES);
+  printf("pace_kv C ABI check passed: %d layers x %d pages of %d B packed and unpacked, sent through "
+         "a channel, and staged through pinned host memory\n", LAYERS, N, PAGE_BYTES);
   return 0;
 }
