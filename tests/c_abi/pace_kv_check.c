@@ -8,7 +8,9 @@
  * further destination pages, and checks them the same way.  Then moves the
  * same pages through pinned host memory with a stager (pack to host, unpack
  * from host, round trip), once with one chunk of all layers and once with a
- * chunk per layer, checking the host bytes and both pools.  Also checks that
+ * chunk per layer, checking the host bytes and both pools.  Then swaps the
+ * same pages out to a pinned host pool and back into zeroed destination
+ * pages, checking the host pool and the destination.  Also checks that
  * an argument error returns PACE_KV_EINVAL with a message.  Exit status 0
  * means every check passed.
  *
@@ -247,6 +249,72 @@ int main(void) {
     for (s = 0; s < 2; ++s) HIP_OK(hipFree(ids_sets[s]));
   }
 
+  /* swap out to a pinned host pool (src[l][src_ids[j]] -> host[l][host_ids[j]]),
+     then into zeroed destination pages (host[l][host_ids[j]] -> dst[l][in_ids[j]]) */
+  {
+    const int32_t host_ids[N] = {7, 2, 5, 0};
+    const int32_t in_ids[N] = {13, 6, 10, 15};
+    const int host_pages = 8;
+    const size_t host_pool_bytes = (size_t)host_pages * PAGE_BYTES;
+    void* host_layers[LAYERS];
+    void *ids_host = NULL, *ids_in = NULL;
+    HIP_OK(hipMalloc(&ids_host, sizeof(host_ids)));
+    HIP_OK(hipMalloc(&ids_in, sizeof(in_ids)));
+    HIP_OK(hipMemcpy(ids_host, host_ids, sizeof(host_ids), hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(ids_in, in_ids, sizeof(in_ids), hipMemcpyHostToDevice));
+    for (l = 0; l < LAYERS; ++l) {
+      HIP_OK(hipHostMalloc(&host_layers[l], host_pool_bytes, 0));
+      memset(host_layers[l], 0, host_pool_bytes);
+      for (j = 0; j < N; ++j) {
+        HIP_OK(hipMemset((char*)dst_layers[l] + (size_t)in_ids[j] * PAGE_BYTES, 0, PAGE_BYTES));
+        memset(host_dst[l] + (size_t)in_ids[j] * PAGE_BYTES, 0, PAGE_BYTES);
+      }
+    }
+    HIP_OK(hipDeviceSynchronize());
+    rc = pace_kv_swap_out((const void* const*)src_layers, POOL_PAGES, (const int32_t*)ids_src, host_layers,
+                          host_pages, (const int32_t*)ids_host, LAYERS, N, PAGE_BYTES, NULL, NULL);
+    if (rc == PACE_KV_OK) {
+      HIP_OK(hipDeviceSynchronize());
+      for (l = 0; l < LAYERS; ++l)
+        for (p = 0; p < host_pages; ++p) {
+          const unsigned char* want = NULL;
+          for (j = 0; j < N; ++j)
+            if (host_ids[j] == p) want = host_src[l] + (size_t)src_ids[j] * PAGE_BYTES;
+          const unsigned char* have = (const unsigned char*)host_layers[l] + (size_t)p * PAGE_BYTES;
+          int bad = 0;
+          if (want != NULL) {
+            bad = memcmp(have, want, PAGE_BYTES) != 0;
+          } else {
+            for (j = 0; j < PAGE_BYTES && !bad; ++j) bad = have[j] != 0;
+          }
+          if (bad) {
+            fprintf(stderr, "swap out: host layer %d page %d differs\n", l, p);
+            ++failures;
+          }
+        }
+      rc = pace_kv_swap_in((const void* const*)host_layers, host_pages, (const int32_t*)ids_host, dst_layers,
+                           POOL_PAGES, (const int32_t*)ids_in, LAYERS, N, PAGE_BYTES, NULL, NULL);
+    }
+    if (rc != PACE_KV_OK) {
+      fprintf(stderr, "swap status %d: %s\n", rc, pace_kv_last_error());
+      return 1;
+    }
+    HIP_OK(hipDeviceSynchronize());
+    for (l = 0; l < LAYERS; ++l) {
+      for (j = 0; j < N; ++j)
+        memcpy(host_dst[l] + (size_t)in_ids[j] * PAGE_BYTES, host_src[l] + (size_t)src_ids[j] * PAGE_BYTES,
+               PAGE_BYTES);
+      HIP_OK(hipMemcpy(got, dst_layers[l], pool_bytes, hipMemcpyDeviceToHost));
+      if (memcmp(got, host_dst[l], pool_bytes) != 0) {
+        fprintf(stderr, "destination layer %d differs after the swap in\n", l);
+        ++failures;
+      }
+      HIP_OK(hipHostFree(host_layers[l]));
+    }
+    HIP_OK(hipFree(ids_host));
+    HIP_OK(hipFree(ids_in));
+  }
+
   /* an argument error is caught on the host, before any launch */
   rc = pace_kv_pack((const void* const*)src_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_src, N, 100,
                     buf, (int64_t)N * PAGE_BYTES, NULL, NULL);
@@ -269,6 +337,6 @@ int main(void) {
   free(got);
   if (failures) return 1;
   printf("pace_kv C ABI check passed: %d layers x %d pages of %d B packed and unpacked, sent through "
-         "a channel, and staged through pinned host memory\n", LAYERS, N, PAGE_BYTES);
+         "a channel, staged through pinned host memory, and swapped out and in\n", LAYERS, N, PAGE_BYTES);
   return 0;
 }
