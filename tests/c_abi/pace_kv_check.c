@@ -10,7 +10,10 @@
  * from host, round trip), once with one chunk of all layers and once with a
  * chunk per layer, checking the host bytes and both pools.  Then swaps the
  * same pages out to a pinned host pool and back into zeroed destination
- * pages, checking the host pool and the destination.  Also checks that
+ * pages, checking the host pool and the destination.  Then appends three
+ * tokens (two requests, one launch with positions derived in the kernel) into
+ * the destination's first layer, read as [pages, 2, 16, 128 B rows], and
+ * checks every layer against the rows placed by hand.  Also checks that
  * an argument error returns PACE_KV_EINVAL with a message.  Exit status 0
  * means every check passed.
  *
@@ -315,6 +318,62 @@ int main(void) {
     HIP_OK(hipFree(ids_in));
   }
 
+  /* paged append into layer 0: request 0 holds pages {2, 9} with 5 tokens in
+     the last (21 tokens after its 2 new ones: positions 19, 20 -> page 9 slots
+     3, 4); request 1 holds page {14} with 1 token (its new one: page 14 slot 0) */
+  {
+    enum { P = 16, ROW = PAGE_BYTES / (2 * P), NNZ = 3, BATCH = 2 };
+    const int32_t append_indptr[BATCH + 1] = {0, 2, 3};
+    const int32_t kv_indptr[BATCH + 1] = {0, 2, 3};
+    const int32_t kv_indices[3] = {2, 9, 14};
+    const int32_t last_len[BATCH] = {5, 1};
+    const int32_t where[NNZ][2] = {{9, 3}, {9, 4}, {14, 0}};   /* page, slot of token i */
+    unsigned char keys[NNZ * ROW], values[NNZ * ROW];
+    void *d_keys, *d_values, *d_ai, *d_ip, *d_idx, *d_last;
+    for (j = 0; j < NNZ * ROW; ++j) {
+      keys[j] = (unsigned char)(j * 5 + 1);
+      values[j] = (unsigned char)(j * 3 + 200);
+    }
+    HIP_OK(hipMalloc(&d_keys, sizeof(keys)));
+    HIP_OK(hipMalloc(&d_values, sizeof(values)));
+    HIP_OK(hipMalloc(&d_ai, sizeof(append_indptr)));
+    HIP_OK(hipMalloc(&d_ip, sizeof(kv_indptr)));
+    HIP_OK(hipMalloc(&d_idx, sizeof(kv_indices)));
+    HIP_OK(hipMalloc(&d_last, sizeof(last_len)));
+    HIP_OK(hipMemcpy(d_keys, keys, sizeof(keys), hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(d_values, values, sizeof(values), hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(d_ai, append_indptr, sizeof(append_indptr), hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(d_ip, kv_indptr, sizeof(kv_indptr), hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(d_idx, kv_indices, sizeof(kv_indices), hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(d_last, last_len, sizeof(last_len), hipMemcpyHostToDevice));
+    rc = pace_kv_append_indptr(d_keys, d_values, ROW, NNZ, (const int32_t*)d_ai, BATCH, dst_layers[0], POOL_PAGES,
+                               (const int32_t*)d_idx, 3, (const int32_t*)d_ip, (const int32_t*)d_last, P, ROW,
+                               NULL, NULL);
+    if (rc != PACE_KV_OK) {
+      fprintf(stderr, "append status %d: %s\n", rc, pace_kv_last_error());
+      return 1;
+    }
+    HIP_OK(hipDeviceSynchronize());
+    for (j = 0; j < NNZ; ++j) {
+      unsigned char* page = host_dst[0] + (size_t)where[j][0] * PAGE_BYTES;
+      memcpy(page + (size_t)where[j][1] * ROW, keys + (size_t)j * ROW, ROW);
+      memcpy(page + (size_t)(P + where[j][1]) * ROW, values + (size_t)j * ROW, ROW);
+    }
+    for (l = 0; l < LAYERS; ++l) {
+      HIP_OK(hipMemcpy(got, dst_layers[l], pool_bytes, hipMemcpyDeviceToHost));
+      if (memcmp(got, host_dst[l], pool_bytes) != 0) {
+        fprintf(stderr, "destination layer %d differs after the append\n", l);
+        ++failures;
+      }
+    }
+    HIP_OK(hipFree(d_keys));
+    HIP_OK(hipFree(d_values));
+    HIP_OK(hipFree(d_ai));
+    HIP_OK(hipFree(d_ip));
+    HIP_OK(hipFree(d_idx));
+    HIP_OK(hipFree(d_last));
+  }
+
   /* an argument error is caught on the host, before any launch */
   rc = pace_kv_pack((const void* const*)src_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_src, N, 100,
                     buf, (int64_t)N * PAGE_BYTES, NULL, NULL);
@@ -337,6 +396,6 @@ int main(void) {
   free(got);
   if (failures) return 1;
   printf("pace_kv C ABI check passed: %d layers x %d pages of %d B packed and unpacked, sent through "
-         "a channel, staged through pinned host memory, and swapped out and in\n", LAYERS, N, PAGE_BYTES);
+         "a channel, staged through pinned host memory, swapped out and in, and appended\n", LAYERS, N, PAGE_BYTES);
   return 0;
 }
