@@ -13,7 +13,8 @@
  * pages, checking the host pool and the destination.  Then appends three
  * tokens (two requests, one launch with positions derived in the kernel) into
  * the destination's first layer, read as [pages, 2, 16, 128 B rows], and
- * checks every layer against the rows placed by hand.  Also checks that
+ * checks every layer against the rows placed by hand, and moves the source
+ * pages into zeroed destination pages with the fused move.  Also checks that
  * an argument error returns PACE_KV_EINVAL with a message.  Exit status 0
  * means every check passed.
  *
@@ -374,6 +375,38 @@ int main(void) {
     HIP_OK(hipFree(d_last));
   }
 
+  /* fused move: src[l][src_ids[j]] -> dst[l][move_ids[j]], no buffer */
+  {
+    const int32_t move_ids[N] = {0, 3, 5, 11};
+    void* ids_move = NULL;
+    HIP_OK(hipMalloc(&ids_move, sizeof(move_ids)));
+    HIP_OK(hipMemcpy(ids_move, move_ids, sizeof(move_ids), hipMemcpyHostToDevice));
+    for (l = 0; l < LAYERS; ++l)
+      for (j = 0; j < N; ++j) {
+        HIP_OK(hipMemset((char*)dst_layers[l] + (size_t)move_ids[j] * PAGE_BYTES, 0, PAGE_BYTES));
+        memset(host_dst[l] + (size_t)move_ids[j] * PAGE_BYTES, 0, PAGE_BYTES);
+      }
+    HIP_OK(hipDeviceSynchronize());
+    rc = pace_kv_move((const void* const*)src_layers, POOL_PAGES, (const int32_t*)ids_src, dst_layers, POOL_PAGES,
+                      (const int32_t*)ids_move, LAYERS, N, PAGE_BYTES, NULL, NULL);
+    if (rc != PACE_KV_OK) {
+      fprintf(stderr, "move status %d: %s\n", rc, pace_kv_last_error());
+      return 1;
+    }
+    HIP_OK(hipDeviceSynchronize());
+    for (l = 0; l < LAYERS; ++l) {
+      for (j = 0; j < N; ++j)
+        memcpy(host_dst[l] + (size_t)move_ids[j] * PAGE_BYTES, host_src[l] + (size_t)src_ids[j] * PAGE_BYTES,
+               PAGE_BYTES);
+      HIP_OK(hipMemcpy(got, dst_layers[l], pool_bytes, hipMemcpyDeviceToHost));
+      if (memcmp(got, host_dst[l], pool_bytes) != 0) {
+        fprintf(stderr, "destination layer %d differs after the move\n", l);
+        ++failures;
+      }
+    }
+    HIP_OK(hipFree(ids_move));
+  }
+
   /* an argument error is caught on the host, before any launch */
   rc = pace_kv_pack((const void* const*)src_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_src, N, 100,
                     buf, (int64_t)N * PAGE_BYTES, NULL, NULL);
@@ -396,6 +429,6 @@ int main(void) {
   free(got);
   if (failures) return 1;
   printf("pace_kv C ABI check passed: %d layers x %d pages of %d B packed and unpacked, sent through "
-         "a channel, staged through pinned host memory, swapped out and in, and appended\n", LAYERS, N, PAGE_BYTES);
+         "a channel, staged through pinned host memory, swapped out and in, appended and moved\n", LAYERS, N, PAGE_BYTES);
   return 0;
 }
