@@ -14,7 +14,8 @@
  * tokens (two requests, one launch with positions derived in the kernel) into
  * the destination's first layer, read as [pages, 2, 16, 128 B rows], and
  * checks every layer against the rows placed by hand, and moves the source
- * pages into zeroed destination pages with the fused move.  Also checks that
+ * pages into zeroed destination pages with the fused move, and packs them to
+ * pinned host memory with the allocation-free entry point.  Also checks that
  * an argument error returns PACE_KV_EINVAL with a message.  Exit status 0
  * means every check passed.
  *
@@ -407,6 +408,32 @@ int main(void) {
     HIP_OK(hipFree(ids_move));
   }
 
+  /* the allocation-free pack into pinned host memory, twice in a row */
+  {
+    const size_t payload = (size_t)LAYERS * N * PAGE_BYTES;
+    void* out = NULL;
+    int rep;
+    HIP_OK(hipHostMalloc(&out, payload, 0));
+    for (rep = 0; rep < 2; ++rep) {
+      memset(out, 0, payload);
+      rc = pace_kv_pack_to_host_noalloc((const void* const*)src_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_src, N,
+                                        PAGE_BYTES, out, (int64_t)payload, NULL, NULL);
+      if (rc != PACE_KV_OK) {
+        fprintf(stderr, "pack_to_host_noalloc status %d: %s\n", rc, pace_kv_last_error());
+        return 1;
+      }
+      HIP_OK(hipDeviceSynchronize());
+      for (l = 0; l < LAYERS; ++l)
+        for (j = 0; j < N; ++j)
+          if (memcmp((unsigned char*)out + ((size_t)l * N + j) * PAGE_BYTES,
+                     host_src[l] + (size_t)src_ids[j] * PAGE_BYTES, PAGE_BYTES) != 0) {
+            fprintf(stderr, "pack_to_host_noalloc call %d: layer %d page %d differs\n", rep, l, j);
+            ++failures;
+          }
+    }
+    HIP_OK(hipHostFree(out));
+  }
+
   /* an argument error is caught on the host, before any launch */
   rc = pace_kv_pack((const void* const*)src_layers, LAYERS, POOL_PAGES, (const int32_t*)ids_src, N, 100,
                     buf, (int64_t)N * PAGE_BYTES, NULL, NULL);
@@ -429,6 +456,6 @@ int main(void) {
   free(got);
   if (failures) return 1;
   printf("pace_kv C ABI check passed: %d layers x %d pages of %d B packed and unpacked, sent through "
-         "a channel, staged through pinned host memory, swapped out and in, appended and moved\n", LAYERS, N, PAGE_BYTES);
+         "a channel, staged through pinned host memory, swapped out and in, appended, moved and packed without allocating\n", LAYERS, N, PAGE_BYTES);
   return 0;
 }
