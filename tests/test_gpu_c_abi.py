@@ -1,7 +1,9 @@
 """The library used from C alone: tests/c_abi/pace_kv_check (built by
-paceserve_amd.build next to its source) packs and unpacks pages and sends
-them through a cross-process channel, through include/pace_kv.h with the HIP
-runtime, and checks every byte on the host."""
+paceserve_amd.build next to its source) packs and unpacks pages, sends them
+through a cross-process channel, stages them through pinned host memory,
+swaps them out and in, appends tokens, moves pages and packs them without
+allocating, through include/pace_kv.h with the HIP runtime, and checks every
+byte on the host."""
 import json
 import subprocess
 
@@ -17,7 +19,9 @@ def test_c_program_packs_and_unpacks_through_the_header(gpu):
         pytest.fail(f"{C_CHECK_BIN} is not built (run python -m paceserve_amd.build)")
     r = subprocess.run([str(C_CHECK_BIN)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert "C ABI check passed" in r.stdout and "channel" in r.stdout
+    assert "C ABI check passed" in r.stdout
+    for leg in ("channel", "staged", "swapped", "appended", "moved", "without allocating"):
+        assert leg in r.stdout, leg
 
 
 def test_c_promote_latency_program_moves_the_right_bytes(gpu):
